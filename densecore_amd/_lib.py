@@ -1,0 +1,68 @@
+"""ctypes binding of ``libdcattn.so`` (the C ABI in ``include/dc_attn.h``).
+
+The library is built in-tree (``densecore_amd/libdcattn.so``) by ``densecore_amd.build``.
+If it is missing, every entry point raises: there is no CPU fallback on this path.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdcattn.so")
+
+DC_OK, DC_INVALID_ARGUMENT, DC_UNSUPPORTED, DC_EXECUTION_FAILED = 0, 1, 2, 3
+DC_F32, DC_BF16 = 0, 1
+
+# Every symbol include/dc_attn.h declares.
+EXPORTS = ("dc_abi_version", "dc_last_error",
+           "dc_sdpa_fwd_workspace_size", "dc_sdpa_fwd",
+           "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
+           "dc_sdpa_decode_workspace_size", "dc_sdpa_decode")
+
+
+class Desc(ctypes.Structure):
+    """``dc_attn_desc``."""
+    _fields_ = [("batch", ctypes.c_int64), ("heads", ctypes.c_int64), ("kv_heads", ctypes.c_int64),
+                ("q_len", ctypes.c_int64), ("kv_len", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+                ("causal", ctypes.c_int32), ("has_scale", ctypes.c_int32), ("scale", ctypes.c_double),
+                ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("mask_stride_b", ctypes.c_int64), ("mask_stride_h", ctypes.c_int64),
+                ("mask_stride_l", ctypes.c_int64)]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"densecore_amd: HIP library not built ({LIB_PATH}); "
+                               "run densecore_amd.build.build() (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        P, SZ, D = ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(Desc)
+        L.dc_abi_version.restype = ctypes.c_int
+        L.dc_last_error.restype = ctypes.c_char_p
+        for name in ("dc_sdpa_fwd_workspace_size", "dc_sdpa_bwd_workspace_size",
+                     "dc_sdpa_decode_workspace_size"):
+            getattr(L, name).argtypes = [D]
+            getattr(L, name).restype = SZ
+        L.dc_sdpa_fwd.argtypes = [D, P, P, P, P, P, P, P, SZ, P]
+        L.dc_sdpa_bwd.argtypes = [D, P, P, P, P, P, P, P, P, P, P, P, SZ, P]
+        L.dc_sdpa_decode.argtypes = [D, P, P, P, P, P, P, SZ, P]
+        for name in ("dc_sdpa_fwd", "dc_sdpa_bwd", "dc_sdpa_decode"):
+            getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def check(status):
+    """Map a dc_status to the exception the reference raises for it (src/lib.rs:555-683)."""
+    if status == DC_OK:
+        return
+    msg = lib().dc_last_error().decode()
+    if status == DC_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    if status == DC_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

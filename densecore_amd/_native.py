@@ -1,0 +1,143 @@
+"""Device-side counterpart of DenseCore's native flash-attention boundary.
+
+``_flash_attention`` and ``_flash_attention_backward`` keep the names, argument meaning and
+error behaviour of the reference's pyo3 functions (``src/lib.rs:555-683``): rank and shape
+checks raise ``ValueError`` with the same messages, kernel failures raise ``RuntimeError``,
+and the results are fresh tensors.  The difference is where the data lives: tensors are
+device-resident ``torch`` tensors on the GPU (torch is used for device memory and streams
+only), and the work is done by the HIP kernels behind ``include/dc_attn.h``.  Calls are
+ordered on torch's current stream of the tensors' device.
+
+``_flash_decode`` is the new single-query entry point (split-KV), equivalent to
+``_flash_attention`` at L = 1 without causal masking.
+"""
+import math
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.DC_F32, torch.bfloat16: _lib.DC_BF16}
+
+
+def _attention_dims(q, k, v):
+    """``attention_dims`` (src/lib.rs:555-580)."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("flash attention takes (B, H, L, E) tensors")
+    qs, ks = tuple(q.shape), tuple(k.shape)
+    ok = ks == tuple(v.shape) and ks[0] == qs[0] and ks[3] == qs[3] and ks[1] > 0 and qs[1] % ks[1] == 0
+    if not ok:
+        raise ValueError("flash attention q/k/v shapes do not match")
+    return qs[0], qs[1], ks[1], qs[2], ks[2], qs[3]
+
+
+def _check_device(*tensors):
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError("flash attention tensors must be on the GPU")
+    dtype = tensors[0].dtype
+    if dtype not in _DTYPES:
+        raise ValueError("flash attention takes float32 or bfloat16 tensors")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError("flash attention tensors must be on one device")
+        if t.dtype != dtype:
+            raise ValueError("flash attention tensors must share one dtype")
+    return dev, dtype
+
+
+def _mask_arg(mask, dims, dev):
+    """``attention_mask`` (src/lib.rs:594-607): an additive float32 (B, H, L, S) mask.
+    Broadcast views (stride 0) are passed through without materialising them."""
+    if mask is None:
+        return None, (0, 0, 0)
+    B, H, _, L, S, _ = dims
+    if tuple(mask.shape) != (B, H, L, S):
+        raise ValueError("flash attention mask must be (B, H, L, S)")
+    if mask.device != dev or mask.dtype != torch.float32:
+        mask = mask.to(device=dev, dtype=torch.float32)
+    if S > 1 and mask.stride(3) != 1:
+        mask = mask.contiguous()
+    return mask, (mask.stride(0), mask.stride(1), mask.stride(2))
+
+
+def _desc(dims, causal, scale, dtype, mstrides):
+    B, H, Hkv, L, S, E = dims
+    return _lib.Desc(B, H, Hkv, L, S, E, int(bool(causal)), int(scale is not None),
+                     float(scale) if scale is not None else 0.0, _DTYPES[dtype], 0, *mstrides)
+
+
+def _ptr(t):
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes, dev):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def _flash_attention(q, k, v, causal, scale=None, mask=None):
+    """Forward: (out, lse).  ``_flash_attention`` (src/lib.rs:609-638)."""
+    dims = _attention_dims(q, k, v)
+    dev, dtype = _check_device(q, k, v)
+    mask, ms = _mask_arg(mask, dims, dev)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    B, H, _, L, _, E = dims
+    out = torch.empty((B, H, L, E), dtype=dtype, device=dev)
+    lse = torch.empty((B, H, L), dtype=torch.float32, device=dev)
+    d = _desc(dims, causal, scale, dtype, ms)
+    L_ = _lib.lib()
+    ws = _workspace(L_.dc_sdpa_fwd_workspace_size(d), dev)
+    _lib.check(L_.dc_sdpa_fwd(d, _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out), _ptr(lse),
+                              _ptr(ws), ws.numel(), _stream(dev)))
+    return out, lse
+
+
+def _flash_attention_backward(grad_out, q, k, v, out, lse, causal, scale=None, mask=None):
+    """Backward: (dq, dk, dv).  ``_flash_attention_backward`` (src/lib.rs:640-683)."""
+    dims = _attention_dims(q, k, v)
+    B, H, Hkv, L, S, E = dims
+    if (tuple(grad_out.shape) != tuple(q.shape) or tuple(out.shape) != tuple(q.shape)
+            or tuple(lse.shape) != (B, H, L)):
+        raise ValueError("flash attention backward shapes do not match")
+    dev, dtype = _check_device(q, k, v, grad_out, out)
+    if lse.device != dev or lse.dtype != torch.float32:
+        raise ValueError("flash attention lse must be float32 on the tensors' device")
+    mask, ms = _mask_arg(mask, dims, dev)
+    grad_out, q, k, v, out, lse = (t.contiguous() for t in (grad_out, q, k, v, out, lse))
+    dq = torch.empty((B, H, L, E), dtype=dtype, device=dev)
+    dk = torch.empty((B, Hkv, S, E), dtype=dtype, device=dev)
+    dv = torch.empty((B, Hkv, S, E), dtype=dtype, device=dev)
+    d = _desc(dims, causal, scale, dtype, ms)
+    L_ = _lib.lib()
+    ws = _workspace(L_.dc_sdpa_bwd_workspace_size(d), dev)
+    _lib.check(L_.dc_sdpa_bwd(d, _ptr(grad_out), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+                              _ptr(mask), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(),
+                              _stream(dev)))
+    return dq, dk, dv
+
+
+def _flash_decode(q, k, v, scale=None):
+    """Single-query attention (q is (B, H, 1, E)) over a contiguous KV cache: (out, lse)."""
+    dims = _attention_dims(q, k, v)
+    dev, dtype = _check_device(q, k, v)
+    B, H, _, L, _, E = dims
+    if L != 1:
+        raise ValueError("flash attention decode takes q_len == 1")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    out = torch.empty((B, H, 1, E), dtype=dtype, device=dev)
+    lse = torch.empty((B, H, 1), dtype=torch.float32, device=dev)
+    d = _desc(dims, False, scale, dtype, (0, 0, 0))
+    L_ = _lib.lib()
+    ws = _workspace(L_.dc_sdpa_decode_workspace_size(d), dev)
+    _lib.check(L_.dc_sdpa_decode(d, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(ws),
+                                 ws.numel(), _stream(dev)))
+    return out, lse
+
+
+def default_scale(head_dim):
+    """``sdp::calculate_scale`` as the Python layer passes it (a double)."""
+    return 1.0 / math.sqrt(head_dim) if head_dim else 1.0

@@ -1,0 +1,204 @@
+// The C ABI declared in include/dc_attn.h: argument checks with the reference's messages,
+// scale computation, workspace carving, and dispatch to the kernel launchers.
+//
+// Checks follow the reference boundary (src/lib.rs:555-580 attention_dims, :594-607
+// attention_mask, :658-663 backward shapes); violations return DC_INVALID_ARGUMENT with the
+// reference's ValueError text.  Launch failures return DC_EXECUTION_FAILED (the reference's
+// RuntimeError, src/lib.rs:633, 677).
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "dc_attn.h"
+#include "params.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+dc_status fail(dc_status st, const std::string &msg) {
+    g_error = msg;
+    return st;
+}
+
+dc_status ok() { return DC_OK; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// A tensor pointer may be null only when the tensor has no elements.
+bool present(const void *p, int64_t count) { return count == 0 || p != nullptr; }
+const char *kNullMsg = "flash attention got a null pointer for a non-empty tensor";
+
+constexpr size_t kAlign = 256;
+size_t round_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+// src/lib.rs:555-580 plus this library's own limits (int32 indexing, head dim).
+dc_status check_dims(const dc_attn_desc *d, dc::AttnShape *s) {
+    if (d == nullptr) return fail(DC_INVALID_ARGUMENT, "flash attention descriptor is null");
+    const int64_t dims[6] = {d->batch, d->heads, d->kv_heads, d->q_len, d->kv_len, d->head_dim};
+    for (int64_t x : dims)
+        if (x < 0) return fail(DC_INVALID_ARGUMENT, "flash attention takes (B, H, L, E) tensors");
+    if (d->kv_heads <= 0 || d->heads % d->kv_heads != 0)
+        return fail(DC_INVALID_ARGUMENT, "flash attention q/k/v shapes do not match");
+    if (d->dtype != DC_F32 && d->dtype != DC_BF16)
+        return fail(DC_INVALID_ARGUMENT, "flash attention dtype must be float32 or bfloat16");
+    for (int64_t x : dims)
+        if (x > INT32_MAX)
+            return fail(DC_UNSUPPORTED, "flash attention dimension exceeds 2^31 - 1");
+    if (d->batch * d->heads > INT32_MAX / 2 || d->batch * d->kv_heads > INT32_MAX / 2)
+        return fail(DC_UNSUPPORTED, "flash attention batch * heads exceeds 2^30");
+    if (d->head_dim > 128)
+        return fail(DC_UNSUPPORTED, "flash attention head_dim above 128 is not implemented");
+    s->B = (int)d->batch;
+    s->H = (int)d->heads;
+    s->Hkv = (int)d->kv_heads;
+    s->L = (int)d->q_len;
+    s->S = (int)d->kv_len;
+    s->E = (int)d->head_dim;
+    s->repeat = s->H / s->Hkv;
+    // sdp::calculate_scale, src/torch_attention.rs:37-40: double, stored as float.
+    s->scale = d->has_scale ? (float)d->scale : (float)(1.0 / std::sqrt((double)d->head_dim));
+    s->scale_log2 = s->scale * 1.4426950408889634f;
+    s->causal = d->causal != 0;
+    s->mask = nullptr;
+    s->msb = s->msh = s->msl = 0;
+    s->vec = true;
+    return ok();
+}
+
+// src/lib.rs:594-607: the reference takes exactly a (B, H, L, S) mask; strides generalise it.
+dc_status check_mask(const dc_attn_desc *d, const float *mask, dc::AttnShape *s) {
+    if (mask == nullptr) return ok();
+    if (d->mask_stride_b < 0 || d->mask_stride_h < 0 || d->mask_stride_l < 0)
+        return fail(DC_INVALID_ARGUMENT, "flash attention mask must be (B, H, L, S)");
+    s->mask = mask;
+    s->msb = d->mask_stride_b;
+    s->msh = d->mask_stride_h;
+    s->msl = d->mask_stride_l;
+    return ok();
+}
+
+dc_status launched(hipError_t e) {
+    if (e != hipSuccess) return fail(DC_EXECUTION_FAILED, std::string("HIP launch failed: ") +
+                                                             hipGetErrorString(e));
+    return ok();
+}
+
+size_t bwd_ws(const dc::AttnShape &s, bool bf16) {
+    size_t n = round_up((size_t)s.B * s.H * s.L * sizeof(float));  // dsum
+    if (bf16) n += round_up((size_t)s.B * s.H * s.L * s.E * sizeof(float));  // dq accumulator
+    return n;
+}
+
+size_t decode_ws(const dc::AttnShape &s) {
+    int split_len = 0;
+    const int splits = dc::decode_splits(s, &split_len);
+    return round_up((size_t)s.B * s.H * splits * (s.E + 2) * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" {
+
+int dc_abi_version(void) { return 1; }
+
+const char *dc_last_error(void) { return g_error.c_str(); }
+
+size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d) {
+    (void)d;
+    return 0;
+}
+
+dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                      const float *mask, void *out, float *lse, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    dc::AttnShape s;
+    dc_status st = check_dims(d, &s);
+    if (st != DC_OK) return st;
+    if ((st = check_mask(d, mask, &s)) != DC_OK) return st;
+    const int64_t nq = (int64_t)s.B * s.H * s.L, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
+    if (nq == 0) return ok();
+    if (!present(q, nq * s.E) || !present(k, nkv) || !present(v, nkv) ||
+        !present(out, nq * s.E) || !present(lse, nq))
+        return fail(DC_INVALID_ARGUMENT, kNullMsg);
+    s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    dc::FwdArgs a{s, q, k, v, out, lse};
+    hipStream_t strm = static_cast<hipStream_t>(stream);
+    if (d->dtype == DC_F32) return launched(dc::launch_fwd_f32(a, strm));
+    return launched(dc::launch_fwd_bf16(a, strm));
+}
+
+size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d) {
+    dc::AttnShape s;
+    if (check_dims(d, &s) != DC_OK) return 0;
+    return bwd_ws(s, d->dtype == DC_BF16);
+}
+
+dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q, const void *k,
+                      const void *v, const void *out, const float *lse, const float *mask,
+                      void *dq, void *dk, void *dv, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+    dc::AttnShape s;
+    dc_status st = check_dims(d, &s);
+    if (st != DC_OK) return st;
+    if ((st = check_mask(d, mask, &s)) != DC_OK) return st;
+    const bool bf16 = d->dtype == DC_BF16;
+    if (workspace_bytes < bwd_ws(s, bf16))
+        return fail(DC_INVALID_ARGUMENT, "flash attention backward workspace is too small");
+    const int64_t nq = (int64_t)s.B * s.H * s.L, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
+    if (!present(grad_out, nq * s.E) || !present(q, nq * s.E) || !present(k, nkv) ||
+        !present(v, nkv) || !present(out, nq * s.E) || !present(lse, nq) ||
+        !present(dq, nq * s.E) || !present(dk, nkv) || !present(dv, nkv) ||
+        !present(workspace, (int64_t)bwd_ws(s, bf16)))
+        return fail(DC_INVALID_ARGUMENT, kNullMsg);
+    if (nq == 0 && nkv == 0) return ok();
+    s.vec = aligned16(grad_out) && aligned16(q) && aligned16(k) && aligned16(v) &&
+            aligned16(out) && aligned16(dq) && aligned16(dk) && aligned16(dv);
+    char *ws = static_cast<char *>(workspace);
+    dc::BwdArgs a{};
+    a.s = s;
+    a.dout = grad_out, a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
+    a.dq = dq, a.dk = dk, a.dv = dv;
+    a.dsum = reinterpret_cast<float *>(ws);
+    a.dq_acc = bf16 ? reinterpret_cast<float *>(ws + round_up((size_t)s.B * s.H * s.L * 4))
+                    : static_cast<float *>(dq);
+    hipStream_t strm = static_cast<hipStream_t>(stream);
+    if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
+    return launched(dc::launch_bwd_bf16(a, strm));
+}
+
+size_t dc_sdpa_decode_workspace_size(const dc_attn_desc *d) {
+    dc::AttnShape s;
+    if (check_dims(d, &s) != DC_OK) return 0;
+    return decode_ws(s);
+}
+
+dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                         void *out, float *lse, void *workspace, size_t workspace_bytes,
+                         void *stream) {
+    dc::AttnShape s;
+    dc_status st = check_dims(d, &s);
+    if (st != DC_OK) return st;
+    if (s.L != 1) return fail(DC_INVALID_ARGUMENT, "flash attention decode takes q_len == 1");
+    if (s.causal)
+        return fail(DC_INVALID_ARGUMENT,
+                    "flash attention decode is non-causal (top-left causal at L = 1 sees one key)");
+    if (workspace_bytes < decode_ws(s))
+        return fail(DC_INVALID_ARGUMENT, "flash attention decode workspace is too small");
+    const int64_t nq = (int64_t)s.B * s.H, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
+    if (nq == 0) return ok();
+    if (!present(q, nq * s.E) || !present(k, nkv) || !present(v, nkv) ||
+        !present(out, nq * s.E) || !present(lse, nq) || !present(workspace, 1))
+        return fail(DC_INVALID_ARGUMENT, kNullMsg);
+    s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    dc::DecodeArgs a{};
+    a.s = s;
+    a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
+    a.part = static_cast<float *>(workspace);
+    a.splits = dc::decode_splits(s, &a.split_len);
+    return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// MFMA layouts used throughout (CDNA3/CDNA4 ISA, wave64):
+//   v_mfma_f32_32x32x2_f32 (a, b, c):  A is 32x2, B is 2x32, C is 32x32.
+//     lane l supplies a = A[l % 32][l / 32] and b = B[l / 32][l % 32];
+//     lane l holds C[i][l % 32] in c[r] for i = 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+//   v_mfma_f32_32x32x16_bf16 (a, b, c): A is 32x16, B is 16x32, same C layout;
+//     lane l supplies A[l % 32][8*(l/32) + 0..7] and B[8*(l/32) + 0..7][l % 32].
+// Because the reduction index of an MFMA may be permuted freely (as long as A and B agree),
+// an accumulator C[i][j] (lane <-> column j) can feed the next MFMA directly as its B operand
+// with "row i of C" as the reduction index: step s of a 32x32x2 chain takes register s, which
+// is row perm2(s, l/32) = 8*(s/4) + 4*(l/32) + s%4.  The kernels use this to keep P in
+// registers between the two products of attention.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+#define DEVI __device__ __forceinline__
+
+namespace dc {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+DEVI f32x16 mfma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+DEVI f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row index (within a 32-row MFMA tile) that accumulator register r of this lane holds.
+DEVI int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// v_exp_f32 / v_log_f32: base-2, about 1 ulp.
+DEVI float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+DEVI float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
+
+// Combine a value with the one held by lane l ^ 32 (the other half of the wave).
+DEVI float xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
+DEVI float xor32_add(float x) { return x + __shfl_xor(x, 32, 64); }
+
+DEVI float bf16_to_f32(__bf16 x) { return static_cast<float>(x); }
+DEVI __bf16 f32_to_bf16(float x) { return static_cast<__bf16>(x); }  // round to nearest even
+
+template <typename T> DEVI float to_f32(T x);
+template <> DEVI float to_f32<float>(float x) { return x; }
+template <> DEVI float to_f32<__bf16>(__bf16 x) { return static_cast<float>(x); }
+template <typename T> DEVI T from_f32(float x);
+template <> DEVI float from_f32<float>(float x) { return x; }
+template <> DEVI __bf16 from_f32<__bf16>(float x) { return static_cast<__bf16>(x); }
+
+}  // namespace dc

@@ -1,0 +1,272 @@
+// Float32 attention forward on CDNA4 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// Computes what DenseCore's torch_attention::forward computes (src/torch_attention.rs:143-284):
+// out = softmax(scale * q k^T + mask, causal) v and lse = max + ln(sum), with fully masked
+// rows giving out = 0 and lse = 0 (:223-226, :258-264).  The blocking is this kernel's own:
+//
+//   * one workgroup = 4 waves = 128 queries of one (batch, head); each wave owns 32 queries;
+//   * the wave's queries stay in VGPRs as the B operand of S^T = K Q^T (keys x queries), so
+//     every lane owns one query column and the online-softmax state (max, sum) is a scalar per
+//     lane, combined with the other half-wave by one cross-lane exchange;
+//   * K and V tiles of BN keys are staged through LDS (row stride D + 4 floats, which keeps
+//     ds_read_b128 conflict-free), with the next tile's global loads in flight during compute;
+//   * P = exp2(S * scale * log2 e - m) never leaves registers: the S^T accumulator is fed back
+//     as the B operand of O^T += V^T P^T with the reduction index permuted to match.
+//
+// Head dims below the instantiated D are zero-padded on load; keys past S and (causal) keys
+// past the query are -inf before the softmax.
+#include "common.hpp"
+#include "params.hpp"
+
+namespace dc {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBM = 32 * kWaves;
+
+template <int D, int BN>
+struct FwdSmem {
+    float k[BN][D + 4];
+    float v[BN][D + 4];
+};
+
+// Global -> register staging of one K/V tile (fast path: E == D, 16-byte aligned rows).
+template <int D, int BN>
+struct KVStage {
+    static constexpr int C4 = D / 4;
+    static constexpr int N = BN * C4 / kThreads;
+    static_assert(BN * C4 % kThreads == 0, "tile must split evenly over the workgroup");
+    f32x4 k[N], v[N];
+
+    DEVI void load(const float *kb, const float *vb, int n0, int S, int tid) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4, key = n0 + r;
+            if (key < S) {
+                k[j] = *reinterpret_cast<const f32x4 *>(kb + (int64_t)key * D + c);
+                v[j] = *reinterpret_cast<const f32x4 *>(vb + (int64_t)key * D + c);
+            } else {
+                k[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    DEVI void store(FwdSmem<D, BN> &sm, int tid) const {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4;
+            *reinterpret_cast<f32x4 *>(&sm.k[r][c]) = k[j];
+            *reinterpret_cast<f32x4 *>(&sm.v[r][c]) = v[j];
+        }
+    }
+};
+
+// Generic path: any E <= D, any alignment; loads straight into LDS.
+template <int D, int BN>
+DEVI void load_kv_generic(FwdSmem<D, BN> &sm, const float *kb, const float *vb, int n0, int S,
+                          int E, int tid) {
+    for (int i = tid; i < BN * D; i += kThreads) {
+        const int r = i / D, c = i % D, key = n0 + r;
+        const bool ok = key < S && c < E;
+        sm.k[r][c] = ok ? kb[(int64_t)key * E + c] : 0.f;
+        sm.v[r][c] = ok ? vb[(int64_t)key * E + c] : 0.f;
+    }
+}
+
+template <int D, int BN, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(kThreads) void fwd_f32_kernel(FwdArgs a) {
+    constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
+    constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
+    __shared__ FwdSmem<D, BN> sm;
+
+    const AttnShape &s = a.s;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int BH = s.B * s.H;
+    const int nqt = (s.L + kBM - 1) / kBM;
+    const int bid = blockIdx.x;
+    const int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;  // longest causal tiles first
+    const int bh = bid % BH, b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
+    const int q0 = qt * kBM;
+    const int qi = q0 + wave * 32 + lr;  // this lane's query
+    const int wave_last_q = q0 + wave * 32 + 31;
+
+    const float *qp = static_cast<const float *>(a.q);
+    const float *kb = static_cast<const float *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+    const float *vb = static_cast<const float *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+
+    // Queries: lane supplies Q[qi][g*DH + t] for t = 0..DH-1.
+    float qreg[DH];
+    {
+        const float *qrow = qp + ((int64_t)bh * s.L + qi) * s.E;
+        if (s.vec && qi < s.L) {
+#pragma unroll
+            for (int t = 0; t < DH; t += 4) {
+                f32x4 x = *reinterpret_cast<const f32x4 *>(qrow + g * DH + t);
+                qreg[t] = x[0], qreg[t + 1] = x[1], qreg[t + 2] = x[2], qreg[t + 3] = x[3];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < DH; ++t) {
+                const int d = g * DH + t;
+                qreg[t] = (qi < s.L && d < s.E) ? qrow[d] : 0.f;
+            }
+        }
+    }
+    const float *mrow = nullptr;
+    if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
+
+    f32x16 oacc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int kv_end = CAUSAL ? min(q0 + kBM, s.S) : s.S;
+    const int ntiles = (kv_end + BN - 1) / BN;
+
+    KVStage<D, BN> stage;
+    if (s.vec && ntiles > 0) stage.load(kb, vb, 0, s.S, tid);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = t * BN;
+        __syncthreads();  // everyone is done reading the previous tile
+        if (s.vec) {
+            stage.store(sm, tid);
+        } else {
+            load_kv_generic<D, BN>(sm, kb, vb, n0, s.S, s.E, tid);
+        }
+        __syncthreads();
+        if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
+
+        // Which 32-key sub-tiles have any key visible to this wave's queries.
+        bool live[NT];
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+            live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
+
+        // S^T = K Q^T: rows are keys, columns are this wave's 32 queries.
+        f32x16 sacc[NT];
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+#pragma unroll
+        for (int t4 = 0; t4 < DH; t4 += 4) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                if (!live[kt]) continue;
+                const f32x4 kk = *reinterpret_cast<const f32x4 *>(&sm.k[kt * 32 + lr][g * DH + t4]);
+                sacc[kt] = mfma_f32(kk[0], qreg[t4 + 0], sacc[kt]);
+                sacc[kt] = mfma_f32(kk[1], qreg[t4 + 1], sacc[kt]);
+                sacc[kt] = mfma_f32(kk[2], qreg[t4 + 2], sacc[kt]);
+                sacc[kt] = mfma_f32(kk[3], qreg[t4 + 3], sacc[kt]);
+            }
+        }
+
+        // Scores in log2 units, masked; tile max per query.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = n0 + kt * 32 + acc_row(r, g);
+                float x;
+                if (MASK) {
+                    const float mv = (key < s.S && qi < s.L) ? mrow[key] : 0.f;
+                    x = (sacc[kt][r] * s.scale + mv) * kLog2e;
+                } else {
+                    x = sacc[kt][r] * s.scale_log2;
+                }
+                if (key >= s.S || (CAUSAL && key > qi) || !live[kt]) x = -INFINITY;
+                sacc[kt][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+        mx = xor32_max(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = exp2_fast(m_run - m_use);
+        float ls = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = exp2_fast(sacc[kt][r] - m_use);
+                sacc[kt][r] = p;
+                ls += p;
+            }
+        ls = xor32_add(ls);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+
+        // O^T += V^T P^T: A = V[key][d] from LDS, B = P straight from the S^T accumulator.
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+            if (!live[kt]) continue;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    oacc[dt] = mfma_f32(sm.v[kt * 32 + acc_row(r, g)][dt * 32 + lr], sacc[kt][r],
+                                        oacc[dt]);
+        }
+    }
+
+    if (qi < s.L) {
+        const bool empty = l_run == 0.f;
+        const float inv = empty ? 0.f : 1.f / l_run;
+        float *orow = static_cast<float *>(a.out) + ((int64_t)bh * s.L + qi) * s.E;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+                const int d = dt * 32 + acc_row(r, g);
+                if (s.vec) {
+                    f32x4 o = {oacc[dt][r] * inv, oacc[dt][r + 1] * inv, oacc[dt][r + 2] * inv,
+                               oacc[dt][r + 3] * inv};
+                    *reinterpret_cast<f32x4 *>(orow + d) = o;
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (d + u < s.E) orow[d + u] = oacc[dt][r + u] * inv;
+                }
+            }
+        if (g == 0)
+            a.lse[(int64_t)bh * s.L + qi] = empty ? 0.f : (m_run + log2_fast(l_run)) * kLn2;
+    }
+}
+
+template <int D, int BN>
+hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
+    FwdArgs a = args;
+    a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked alignment; E must fill D
+    const int nqt = (a.s.L + kBM - 1) / kBM;
+    const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
+    const bool mask = a.s.mask != nullptr;
+    if (a.s.causal && mask)
+        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, true, true>), grid, block, 0, st, a);
+    else if (a.s.causal)
+        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, true, false>), grid, block, 0, st, a);
+    else if (mask)
+        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, false, true>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, false, false>), grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st) {
+    if (a.s.B == 0 || a.s.H == 0 || a.s.L == 0) return hipSuccess;
+    if (a.s.E <= 32) return launch_d<32, 64>(a, st);
+    if (a.s.E <= 64) return launch_d<64, 64>(a, st);
+    return launch_d<128, 32>(a, st);
+}
+
+}  // namespace dc

@@ -1,0 +1,95 @@
+/*
+ * dc_attn.h — C ABI of the MI355X (gfx950) scaled-dot-product-attention library
+ * (libdcattn.so, built from densecore_amd/csrc).
+ *
+ * This is the drop-in boundary for DenseCore's flash-attention path.  It replaces the two
+ * pyo3 entry points of the reference and the CPU kernels behind them:
+ *
+ *   dc_sdpa_fwd     replaces  _flash_attention           src/lib.rs:609-638
+ *                             -> torch_attention::forward  src/torch_attention.rs:143-284
+ *   dc_sdpa_bwd     replaces  _flash_attention_backward  src/lib.rs:640-683
+ *                             -> torch_attention::backward src/torch_attention.rs:286-468
+ *   dc_sdpa_decode  single-query attention; in the reference this is forward() with L = 1,
+ *                   non-causal (src/torch_attention.rs:157, 176-180); here it is a split-KV
+ *                   kernel pair
+ *   dc_last_error   the message the reference would raise (src/lib.rs:561-571, 601-605,
+ *                   633, 658-662, 677)
+ *
+ * Conventions (the reference's, src/torch_attention.rs:7 and src/lib.rs:555-607):
+ *   q, out, grad_out, dq : contiguous row-major (B, H, L, E)
+ *   k, v, dk, dv         : contiguous row-major (B, Hkv, S, E), H % Hkv == 0 (grouped heads)
+ *   lse                  : contiguous (B, H, L), float32, natural log
+ *   mask                 : optional additive float32 mask indexed (b, h, l, s) at
+ *                          b*mask_stride_b + h*mask_stride_h + l*mask_stride_l + s; the
+ *                          reference's (B, H, L, S) contiguous mask has strides
+ *                          (H*L*S, L*S, S); a stride of 0 broadcasts that dimension
+ *   causal               : top-left aligned, key s visible to query l iff s <= l
+ *   scale                : has_scale ? (float)scale : (float)(1 / sqrt((double)E))
+ *   fully masked row     : out = 0, lse = 0, and zero gradients
+ *
+ * All pointers are device pointers (hipMalloc'd or equivalent).  Calls are asynchronous and
+ * ordered on `stream` (a hipStream_t; NULL is the null stream).  The caller owns every buffer;
+ * workspaces are sized by the matching *_workspace_size call and must be 256-byte aligned.
+ * The library keeps no global mutable state except the thread-local last error.
+ */
+#ifndef DC_ATTN_H
+#define DC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    DC_OK = 0,
+    DC_INVALID_ARGUMENT = 1, /* shape / argument errors: the reference raises ValueError */
+    DC_UNSUPPORTED = 2,      /* outside what the kernels implement (e.g. E > 256) */
+    DC_EXECUTION_FAILED = 3  /* a HIP launch or runtime error: the reference's RuntimeError */
+} dc_status;
+
+typedef enum { DC_F32 = 0, DC_BF16 = 1 } dc_dtype;
+
+typedef struct {
+    int64_t batch, heads, kv_heads, q_len, kv_len, head_dim;
+    int32_t causal;    /* 0 / 1 */
+    int32_t has_scale; /* 0: scale = 1/sqrt(head_dim), computed in double then rounded */
+    double scale;
+    int32_t dtype;     /* dc_dtype of q, k, v, out, grad_out, dq, dk, dv (lse is float32) */
+    int32_t reserved;
+    int64_t mask_stride_b, mask_stride_h, mask_stride_l; /* elements; used when mask != NULL */
+} dc_attn_desc;
+
+/* Version of this ABI (bumped on any incompatible change). */
+int dc_abi_version(void);
+
+/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284. */
+size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d);
+dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                      const float *mask, void *out, float *lse, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* Backward (dq, dk, dv) from the saved out and lse.  src/lib.rs:640-683,
+ * src/torch_attention.rs:286-468. */
+size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d);
+dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q, const void *k,
+                      const void *v, const void *out, const float *lse, const float *mask,
+                      void *dq, void *dk, void *dv, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* Single-query (q_len == 1), non-causal attention over a contiguous KV cache, split over the
+ * keys and merged.  Same results as dc_sdpa_fwd at q_len == 1 (the reference's decode). */
+size_t dc_sdpa_decode_workspace_size(const dc_attn_desc *d);
+dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                         void *out, float *lse, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
+/* Message of the last non-DC_OK status on the calling thread ("" if none). */
+const char *dc_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DC_ATTN_H */

@@ -1,0 +1,188 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes front end of the CPU oracle (``sdpa_oracle.c``).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
+this package, and only as the checker (or the timed CPU baseline).  The product package
+``densecore_amd`` never imports it.
+
+``forward`` / ``backward`` mirror DenseCore's ``torch_attention::forward`` /
+``torch_attention::backward`` (``src/torch_attention.rs:143-284, 286-468``) on contiguous
+float32 NumPy arrays laid out (B, H, L, E) for q/out/grad_out, (B, Hkv, S, E) for k/v and
+(B, H, L) for lse; ``mask`` is the additive float (B, H, L, S) mask the reference's boundary
+accepts (``src/lib.rs:594-607``).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_sdpa.so")
+_lib = None
+
+_F = ctypes.POINTER(ctypes.c_float)
+_SZ = ctypes.c_size_t
+
+ERRORS = {1: "gemm layout outside PyTorch's BLAS path", 2: "out of memory",
+          3: "flash attention q/k/v shapes do not match"}
+
+
+def build(force=False):
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all", "liboracle_sdpa.so"],
+                       check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library not built: {_LIB_PATH} (run oracle.build())")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_forward.argtypes = [_F, _F, _F, _F] + [_SZ] * 6 + [ctypes.c_int, ctypes.c_int,
+                                                                     ctypes.c_double, _F, _F]
+        L.oracle_forward.restype = ctypes.c_int
+        L.oracle_backward.argtypes = [_F] * 7 + [_SZ] * 6 + [ctypes.c_int, ctypes.c_int,
+                                                              ctypes.c_double, _F, _F, _F]
+        L.oracle_backward.restype = ctypes.c_int
+        L.oracle_set_num_threads.argtypes = [_SZ]
+        L.oracle_get_num_threads.restype = _SZ
+        L.oracle_exp_u20.argtypes = [_F, _F, _SZ]
+        L.oracle_sleef_expf.argtypes = [_F, _F, _SZ]
+        L.oracle_reduce_max.argtypes = [_F, _SZ]
+        L.oracle_reduce_max.restype = ctypes.c_float
+        L.oracle_reduce_dot.argtypes = [_F, _F, _SZ]
+        L.oracle_reduce_dot.restype = ctypes.c_float
+        L.oracle_mul_reduce_max.argtypes = [_F, _SZ, ctypes.c_float]
+        L.oracle_mul_reduce_max.restype = ctypes.c_float
+        L.oracle_exp_reduce_sum.argtypes = [_F, _SZ, ctypes.c_float]
+        L.oracle_exp_reduce_sum.restype = ctypes.c_float
+        L.oracle_gemm_raw.argtypes = [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, ctypes.c_float,
+                                      _F, _SZ, _F, _SZ, ctypes.c_float, _F, _SZ]
+        L.oracle_gemm_raw.restype = ctypes.c_int
+        L.oracle_scale_factor.argtypes = [_SZ, ctypes.c_int, ctypes.c_double]
+        L.oracle_scale_factor.restype = ctypes.c_float
+        L.oracle_q_split.argtypes = [_SZ]
+        L.oracle_q_split.restype = _SZ
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(_F)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_num_threads(n):
+    lib().oracle_set_num_threads(int(n))
+
+
+def get_num_threads():
+    return int(lib().oracle_get_num_threads())
+
+
+def _dims(q, k, v):
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("flash attention takes (B, H, L, E) tensors")
+    if not (k.shape == v.shape and k.shape[0] == q.shape[0] and k.shape[3] == q.shape[3]
+            and k.shape[1] > 0 and q.shape[1] % k.shape[1] == 0):
+        raise ValueError("flash attention q/k/v shapes do not match")
+    return q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3]
+
+
+def forward(q, k, v, causal, scale=None, mask=None):
+    """``torch_attention::forward`` (``src/torch_attention.rs:143-284``): (out, lse)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, H, Hkv, L, S, E = _dims(q, k, v)
+    if mask is not None:
+        mask = _f32(mask)
+        if mask.shape != (B, H, L, S):
+            raise ValueError("flash attention mask must be (B, H, L, S)")
+    out = np.empty((B, H, L, E), np.float32)
+    lse = np.empty((B, H, L), np.float32)
+    r = lib().oracle_forward(_p(q), _p(k), _p(v), _p(mask), B, H, Hkv, L, S, E, int(bool(causal)),
+                             int(scale is not None), float(scale or 0.0), _p(out), _p(lse))
+    if r:
+        raise RuntimeError(ERRORS.get(r, f"oracle error {r}"))
+    return out, lse
+
+
+def backward(grad_out, q, k, v, out, lse, causal, scale=None, mask=None):
+    """``torch_attention::backward`` (``src/torch_attention.rs:286-468``): (dq, dk, dv)."""
+    g, q, k, v, o, lse = (_f32(x) for x in (grad_out, q, k, v, out, lse))
+    B, H, Hkv, L, S, E = _dims(q, k, v)
+    if g.shape != q.shape or o.shape != q.shape or lse.shape != (B, H, L):
+        raise ValueError("flash attention backward shapes do not match")
+    if mask is not None:
+        mask = _f32(mask)
+        if mask.shape != (B, H, L, S):
+            raise ValueError("flash attention mask must be (B, H, L, S)")
+    dq = np.empty((B, H, L, E), np.float32)
+    dk = np.empty((B, Hkv, S, E), np.float32)
+    dv = np.empty((B, Hkv, S, E), np.float32)
+    r = lib().oracle_backward(_p(g), _p(q), _p(k), _p(v), _p(o), _p(lse), _p(mask), B, H, Hkv, L, S,
+                              E, int(bool(causal)), int(scale is not None), float(scale or 0.0),
+                              _p(dq), _p(dk), _p(dv))
+    if r:
+        raise RuntimeError(ERRORS.get(r, f"oracle error {r}"))
+    return dq, dk, dv
+
+
+# ---- single functions, for pinning each piece against the mathematics ----
+
+def exp_u20(x):
+    x = _f32(x)
+    assert x.size % 4 == 0
+    y = np.empty_like(x)
+    lib().oracle_exp_u20(_p(x), _p(y), x.size)
+    return y
+
+
+def sleef_expf(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().oracle_sleef_expf(_p(x), _p(y), x.size)
+    return y
+
+
+def reduce_max(x):
+    x = _f32(x)
+    return float(lib().oracle_reduce_max(_p(x), x.size))
+
+
+def reduce_dot(a, b):
+    a, b = _f32(a), _f32(b)
+    return float(lib().oracle_reduce_dot(_p(a), _p(b), a.size))
+
+
+def mul_reduce_max(row, scale):
+    row = _f32(row).copy()
+    m = float(lib().oracle_mul_reduce_max(_p(row), row.size, scale))
+    return row, m
+
+
+def exp_reduce_sum(row, mx):
+    row = _f32(row).copy()
+    s = float(lib().oracle_exp_reduce_sum(_p(row), row.size, mx))
+    return row, s
+
+
+def gemm_raw(ta, tb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
+    a, b = _f32(a), _f32(b)
+    c = _f32(c).copy()
+    r = lib().oracle_gemm_raw(int(ta), int(tb), m, n, k, alpha, _p(a), lda, _p(b), ldb, beta, _p(c), ldc)
+    if r:
+        raise RuntimeError(ERRORS.get(r, f"oracle error {r}"))
+    return c
+
+
+def scale_factor(e, scale=None):
+    return float(lib().oracle_scale_factor(e, int(scale is not None), float(scale or 0.0)))
+
+
+def q_split(q_len):
+    return int(lib().oracle_q_split(q_len))

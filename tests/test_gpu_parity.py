@@ -1,0 +1,177 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on identical inputs.
+
+Tolerance (written here, the target's): float32 outputs, lse and gradients must satisfy
+|gpu - ref| <= 2e-5 + 1e-5 |ref| elementwise.
+
+Shapes are the ones the reference's own tests pin (tests/test_sdpa_exact.py:10-14, 33-41;
+tests/test_attention.py:12-39; tests/test_torch_api_f1.py:78-84) plus the edge cases the
+kernels' tiling creates (partial tiles, head dims that are not a multiple of 4, L != S,
+fully masked rows, one key, grouped heads).
+"""
+import numpy as np
+import pytest
+
+from tests._data import additive, assert_f32
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _run_fwd(q, k, v, causal, scale, mask):
+    from densecore_amd import _native
+    m = None if mask is None else _t(mask)
+    out, lse = _native._flash_attention(_t(q), _t(k), _t(v), causal, scale, m)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), lse.cpu().numpy()
+
+
+def _run_bwd(g, q, k, v, out, lse, causal, scale, mask):
+    from densecore_amd import _native
+    m = None if mask is None else _t(mask)
+    grads = _native._flash_attention_backward(_t(g), _t(q), _t(k), _t(v), _t(out), _t(lse), causal,
+                                              scale, m)
+    torch.cuda.synchronize()
+    return [x.cpu().numpy() for x in grads]
+
+
+def _check(oracle, q, k, v, g, causal, scale=None, mask=None, tag=""):
+    print(f"[case] {tag} q{q.shape} k{k.shape} causal={causal} scale={scale} "
+          f"mask={None if mask is None else mask.shape}", flush=True)
+    ref_o, ref_l = oracle.forward(q, k, v, causal, scale, mask)
+    out, lse = _run_fwd(q, k, v, causal, scale, mask)
+    assert_f32(out, ref_o, f"{tag} out")
+    assert_f32(lse, ref_l, f"{tag} lse")
+    if g is None:
+        return
+    # Backward from the oracle's saved (out, lse), so the gradients are compared on equal inputs.
+    ref = oracle.backward(g, q, k, v, ref_o, ref_l, causal, scale, mask)
+    got = _run_bwd(g, q, k, v, ref_o, ref_l, causal, scale, mask)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_f32(a, b, f"{tag} {name}")
+
+
+EXACT_SHAPES = [  # tests/test_sdpa_exact.py:10-14
+    (2, 2, 7, 7, 5, False, None), (2, 2, 7, 7, 5, True, None), (1, 3, 33, 33, 16, True, None),
+    (1, 2, 100, 37, 12, False, None), (1, 1, 200, 200, 8, True, None), (1, 1, 600, 600, 8, False, None),
+    (1, 1, 800, 800, 4, True, None), (1, 2, 9, 1030, 6, False, None), (1, 2, 64, 64, 16, True, 0.3),
+]
+
+
+@pytest.mark.parametrize("B,H,L,S,E,causal,scale", EXACT_SHAPES)
+def test_exact_shapes(oracle_lib, B, H, L, S, E, causal, scale):
+    rng = np.random.default_rng(L * 31 + S)
+    q, g = (rng.normal(size=(B, H, L, E)).astype(np.float32) for _ in range(2))
+    k, v = (rng.normal(size=(B, H, S, E)).astype(np.float32) for _ in range(2))
+    _check(oracle_lib, q, k, v, g, causal, scale, tag=f"exact{(B, H, L, S, E)}")
+
+
+MASK_SHAPES = [(2, 2, 7, 7, 5), (1, 2, 200, 37, 12), (1, 1, 9, 1030, 6), (2, 3, 64, 64, 16)]
+
+
+@pytest.mark.parametrize("B,H,L,S,E", MASK_SHAPES)
+@pytest.mark.parametrize("kind", ["bool2d", "float2d", "bool4d_b1", "float4d_1h", "row"])
+def test_masked_shapes(oracle_lib, B, H, L, S, E, kind):
+    """tests/test_sdpa_exact.py:32-51: five mask kinds; "row" masks every key of every row."""
+    rng = np.random.default_rng(L + S)
+    q, g = (rng.normal(size=(B, H, L, E)).astype(np.float32) for _ in range(2))
+    k, v = (rng.normal(size=(B, H, S, E)).astype(np.float32) for _ in range(2))
+    mask = {"bool2d": rng.random((L, S)) > 0.3, "float2d": rng.normal(size=(L, S)).astype(np.float32),
+            "bool4d_b1": rng.random((B, 1, L, S)) > 0.5,
+            "float4d_1h": rng.normal(size=(1, H, 1, S)).astype(np.float32),
+            "row": np.zeros((L, S), bool)}[kind]
+    full = additive(mask, (B, H, L, S)) if mask.dtype == np.bool_ else \
+        np.ascontiguousarray(np.broadcast_to(mask, (B, H, L, S)), np.float32)
+    _check(oracle_lib, q, k, v, g, False, None, full, tag=f"mask-{kind}{(B, H, L, S, E)}")
+
+
+@pytest.mark.parametrize("mode", ["none", "causal", "bool", "float"])
+def test_attention_rank4(oracle_lib, mode):
+    """tests/test_attention.py:12-39, rank-4 (2, 3, 4, 8) cases."""
+    rng = np.random.default_rng(21)
+    q, k, v, g = (rng.normal(size=(2, 3, 4, 8)).astype(np.float32) for _ in range(4))
+    mask = None
+    if mode == "bool":
+        m = rng.random((4, 4)) > .3
+        m[:, 0] = True
+        mask = additive(m, (2, 3, 4, 4))
+    elif mode == "float":
+        mask = np.ascontiguousarray(np.broadcast_to(rng.normal(size=(4, 4)).astype(np.float32),
+                                                    (2, 3, 4, 4)))
+    _check(oracle_lib, q, k, v, g, mode == "causal", None, mask, tag=f"rank4-{mode}")
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,E,causal", [
+    (2, 4, 2, 5, 5, 8, True),        # tests/test_torch_api_f1.py:78-84
+    (1, 6, 2, 300, 300, 64, True),
+    (2, 8, 1, 130, 250, 32, False),
+])
+def test_grouped_heads(oracle_lib, B, H, Hkv, L, S, E, causal):
+    rng = np.random.default_rng(B * 1000 + H * 10 + Hkv)
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, Hkv, S, E), dtype=np.float32) for _ in range(2))
+    _check(oracle_lib, q, k, v, g, causal, tag="gqa")
+
+
+@pytest.mark.parametrize("B,H,L,S,E,causal", [
+    (1, 1, 1, 1, 64, False), (1, 2, 1, 700, 64, False), (1, 1, 129, 1, 64, True),
+    (2, 2, 257, 191, 64, True), (1, 3, 191, 257, 64, False), (1, 2, 130, 70, 128, True),
+    (1, 2, 65, 300, 128, False), (1, 1, 40, 40, 100, True), (1, 1, 33, 47, 1, False),
+    (1, 1, 50, 60, 31, True), (3, 1, 200, 200, 64, True),
+])
+def test_tile_edges(oracle_lib, B, H, L, S, E, causal):
+    rng = np.random.default_rng(B + 7 * H + 13 * L + 17 * S + 19 * E)
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, H, S, E), dtype=np.float32) for _ in range(2))
+    _check(oracle_lib, q, k, v, g, causal, tag="edge")
+
+
+def test_causal_with_mask(oracle_lib):
+    """The native boundary accepts causal and a mask together (src/torch_attention.rs:202-215)."""
+    rng = np.random.default_rng(5)
+    q, k, v, g = (rng.standard_normal((2, 2, 150, 64), dtype=np.float32) for _ in range(4))
+    mask = rng.standard_normal((2, 2, 150, 150)).astype(np.float32)
+    _check(oracle_lib, q, k, v, g, True, 0.2, mask, tag="causal+mask")
+
+
+def test_large_logits(oracle_lib):
+    """Scores far past the exp_u20 bound (|x - max| > 87.3, the reference's SLEEF fallback).
+
+    Forward at the standard tolerance.  The gradients of such a peaked softmax are
+    ill-conditioned: a one-ulp change of a score of magnitude ~100 moves P by ~1e-5
+    relative, so two correct float32 summation orders differ by more than 2e-5.  There the
+    GPU is held to float64 truth instead: its error may not exceed twice the oracle's."""
+    from oracle import brute
+    rng = np.random.default_rng(9)
+    q, k, v, g = (rng.standard_normal((1, 2, 96, 64), dtype=np.float32) for _ in range(4))
+    q, k = q * 6, k * 6
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    out, lse = _run_fwd(q, k, v, True, None, None)
+    assert_f32(out, ref_o, "large-logits out")
+    assert_f32(lse, ref_l, "large-logits lse")
+    truth = brute.sdpa_grads(g, q, k, v, True)
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, True)
+    got = _run_bwd(g, q, k, v, ref_o, ref_l, True, None, None)
+    for name, a, b, t in zip(("dq", "dk", "dv"), got, ref, truth):
+        err_gpu, err_ref = np.abs(a - t).max(), np.abs(b - t).max()
+        assert err_gpu <= 2 * err_ref + 2e-6, f"{name}: gpu err {err_gpu:.3e} vs oracle {err_ref:.3e}"
+
+
+def test_errors_match_reference():
+    """src/lib.rs:561-571, 599-606, 658-663: ValueError with the reference's messages."""
+    from densecore_amd import _native
+    x = torch.zeros((1, 2, 3, 4), device=DEV)
+    with pytest.raises(ValueError, match=r"takes \(B, H, L, E\) tensors"):
+        _native._flash_attention(x[0], x, x, False)
+    with pytest.raises(ValueError, match="q/k/v shapes do not match"):
+        _native._flash_attention(x, torch.zeros((1, 3, 3, 4), device=DEV), x, False)
+    with pytest.raises(ValueError, match="mask must be"):
+        _native._flash_attention(x, x, x, False, None, torch.zeros((1, 2, 3, 2), device=DEV))
+    out, lse = _native._flash_attention(x, x, x, False)
+    with pytest.raises(ValueError, match="backward shapes do not match"):
+        _native._flash_attention_backward(out, x, x, x, out, lse[..., :2], False)
