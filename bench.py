@@ -1,0 +1,248 @@
+"""Benchmark of the SDPA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only C2,C4]
+
+A step is one pass of the hot path over one batch of synthetic, HBM-resident input:
+C2 (the headline) is causal fp32 forward + backward at B8 H12 T1024
+D64 through the C ABI (dc_sdpa_fwd then dc_sdpa_bwd).  ``value`` is C2's algorithmic TFLOP/s
+(4*B*H*T^2*D/2 forward, 2.5x that backward).  The same line carries the decode figure the
+metric names (C4, dc_sdpa_decode, GB/s of K + V + q + out + lse), the other configurations'
+throughput, a roofline entry per kernel family timed with HIP events on the launch stream,
+and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense
+PEAK_BF16_MFMA = 2500.0  # TFLOP/s, MI355X dense
+PEAK_HBM = 8000.0        # GB/s
+
+METRIC = "SDPA fwd+bwd TFLOP/s & %MFMA peak (B8 H12 T1024 D64); decode GB/s"
+
+
+def flops(B, H, L, S, E, causal, backward):
+    """Algorithmic FLOPs: 4*B*H*L*S*E (two GEMMs), halved when causal; backward is 2.5x."""
+    f = 4.0 * B * H * L * S * E / (2 if causal else 1)
+    return f, 2.5 * f if backward else 0.0
+
+
+def decode_bytes(B, H, S, E, elem=4):
+    """K + V + q + out (elem bytes each) + lse (float32)."""
+    return 2 * B * H * S * E * elem + 2 * B * H * E * elem + B * H * 4
+
+
+def load_traffic():
+    """Measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    path = os.path.join(HERE, "profiles", "traffic.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f)
+    return {}
+
+
+class Timer:
+    """Accumulates HIP-event durations of calls made on one stream."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream, self.pairs = torch, stream, []
+
+    def __call__(self, fn):
+        t = self.torch
+        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        r = fn()
+        b.record(self.stream)
+        self.pairs.append((a, b))
+        return r
+
+    def mean_ms(self):
+        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) if self.pairs else 0.0
+
+
+def roofline(achieved, peak, unit, bound, traffic, kernel, work_note):
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel,
+            "work": work_note}
+
+
+def bench_prefill(torch, native, name, steps, warmup, dev):
+    """Forward (+ backward) of a prefill config; returns per-call mean ms and throughput."""
+    from tests._data import CONFIGS, make_inputs, additive
+    B, H, L, S, E, causal, bwd, _ = CONFIGS[name]
+    d = make_inputs(name)
+    bf16 = name == "C5"
+    dt = torch.bfloat16 if bf16 else torch.float32
+    q, k, v = (torch.from_numpy(d[n]).to(dev, dt) for n in "qkv")
+    g = torch.from_numpy(d["g"]).to(dev, dt) if bwd else None
+    mask = None
+    if d["mask_bool"] is not None:  # C3: key padding as a broadcast (B, 1, 1, S) additive mask
+        mask = torch.from_numpy(additive(d["mask_bool"], (B, 1, 1, S)).copy()).to(dev).expand(B, H, L, S)
+    scale = 1.0 / np.sqrt(E)
+    stream = torch.cuda.current_stream(dev)
+    tf, tb = Timer(torch, stream), Timer(torch, stream)
+
+    def step(timed):
+        if timed:
+            out, lse = tf(lambda: native._flash_attention(q, k, v, causal, scale, mask))
+            if bwd:
+                tb(lambda: native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask))
+        else:
+            out, lse = native._flash_attention(q, k, v, causal, scale, mask)
+            if bwd:
+                native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask)
+
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    ff, fb = flops(B, H, L, S, E, causal, bwd)
+    if name == "C3":  # useful work counts valid keys only
+        ff = 4.0 * H * L * E * float(np.sum(d["lengths"]))
+    res = {"ms_per_step": wall, "fwd_ms": tf.mean_ms(), "bwd_ms": tb.mean_ms(),
+           "fwd_flop": ff, "bwd_flop": fb}
+    res["tflops"] = (ff + fb) / (wall * 1e-3) / 1e12
+    res["fwd_tflops"] = ff / (res["fwd_ms"] * 1e-3) / 1e12
+    if bwd:
+        res["bwd_tflops"] = fb / (res["bwd_ms"] * 1e-3) / 1e12
+    return res
+
+
+def bench_decode(torch, native, steps, warmup, dev):
+    from tests._data import CONFIGS, make_inputs
+    B, H, L, S, E, _, _, _ = CONFIGS["C4"]
+    d = make_inputs("C4")
+    q, k, v = (torch.from_numpy(d[n]).to(dev) for n in "qkv")
+    del d
+    stream = torch.cuda.current_stream(dev)
+    t = Timer(torch, stream)
+    for _ in range(warmup):
+        native._flash_decode(q, k, v)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        t(lambda: native._flash_decode(q, k, v))
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    nbytes = decode_bytes(B, H, S, E)
+    ev = t.mean_ms()
+    return {"ms_per_step": wall, "event_ms": ev, "bytes": nbytes,
+            "gbps": nbytes / (ev * 1e-3) / 1e9}
+
+
+def cpu_baseline(threads):
+    """The oracle (C port of DenseCore's CPU SDPA) on the full C2 workload, this host's cores."""
+    import oracle
+    from tests._data import make_inputs
+    oracle.build()
+    oracle.set_num_threads(threads)
+    d = make_inputs("C2")
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        o, l = oracle.forward(d["q"], d["k"], d["v"], True)
+        oracle.backward(d["g"], d["q"], d["k"], d["v"], o, l, True)
+        times.append(time.perf_counter() - t0)
+    ff, fb = flops(8, 12, 1024, 1024, 64, True, True)
+    best = float(np.median(times))
+    return {"value": round((ff + fb) / best / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"full C2 fwd+bwd (B8 H12 T1024 D64 fp32) x{len(times)}, median "
+                      f"{best:.2f} s; oracle/sdpa_oracle.c, {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list of configs to run (C1..C5)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "path shards over (batch, head) with no collectives, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import densecore_amd._native as native
+    from densecore_amd import _lib
+    _lib.lib()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+    only = set(args.only.split(",")) if args.only else {"C1", "C2", "C3", "C4", "C5"}
+
+    results = {}
+    for name in ("C2", "C1", "C3", "C5"):
+        if name not in only:
+            continue
+        try:
+            results[name] = bench_prefill(torch, native, name, args.steps, args.warmup, dev)
+        except NotImplementedError as e:
+            results[name] = {"skipped": str(e)}
+        torch.cuda.empty_cache()
+    if "C4" in only:
+        results["C4"] = bench_decode(torch, native, args.steps, args.warmup, dev)
+        torch.cuda.empty_cache()
+
+    traffic = load_traffic()
+    line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1), HBM-resident)",
+            "config": {"workload": "C2: causal SDPA fwd+bwd fp32, B=8 H=12 T=1024 D=64",
+                       "global_batch": 8, "seq_len": 1024, "parallelism": "none (1 GPU)"}}
+    c2 = results.get("C2")
+    if c2:
+        line["value"] = round(c2["tflops"], 3)
+        line["ms_per_step"] = round(c2["ms_per_step"], 4)
+        line["roofline"] = roofline(
+            c2["bwd_tflops"], PEAK_FP32_MFMA, "TFLOP/s", "mfma", traffic.get("C2_bwd"),
+            "dc_sdpa_bwd (bwd_pre_kernel + bwd_f32_kernel)",
+            f"{c2['bwd_flop'] / 1e9:.3f} GFLOP per call / {c2['bwd_ms']:.4f} ms (HIP events)")
+        line["forward_roofline"] = roofline(
+            c2["fwd_tflops"], PEAK_FP32_MFMA, "TFLOP/s", "mfma", traffic.get("C2_fwd"),
+            "dc_sdpa_fwd (fwd_f32_kernel)",
+            f"{c2['fwd_flop'] / 1e9:.3f} GFLOP per call / {c2['fwd_ms']:.4f} ms (HIP events)")
+        line["mfma_frac"] = round(c2["tflops"] / PEAK_FP32_MFMA, 4)
+    c4 = results.get("C4")
+    if c4:
+        line["decode"] = {"workload": "C4: decode fp32, B=32 H=32 S=4096 D=128, split-KV",
+                          "value": round(c4["gbps"], 1), "unit": "GB/s",
+                          "ms_per_step": round(c4["event_ms"], 4),
+                          "roofline": roofline(c4["gbps"], PEAK_HBM, "GB/s", "hbm",
+                                               traffic.get("C4_decode"),
+                                               "dc_sdpa_decode (decode_split + decode_merge)",
+                                               f"{c4['bytes']} B per call / {c4['event_ms']:.4f} ms")}
+    others = {}
+    for name in ("C1", "C3", "C5"):
+        r = results.get(name)
+        if not r:
+            continue
+        if "skipped" in r:
+            others[name] = r
+            continue
+        peak = PEAK_BF16_MFMA if name == "C5" else PEAK_FP32_MFMA
+        others[name] = {"tflops": round(r["tflops"], 3), "ms_per_step": round(r["ms_per_step"], 4),
+                        "frac": round(r["tflops"] / peak, 4), "fwd_ms": round(r["fwd_ms"], 4)}
+        if r.get("bwd_ms"):
+            others[name]["bwd_ms"] = round(r["bwd_ms"], 4)
+    if others:
+        line["other_configs"] = others
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        line["cpu_baseline"] = cpu_baseline(threads)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
