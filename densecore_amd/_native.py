@@ -123,10 +123,10 @@ def _flash_attention_backward(grad_out, q, k, v, out, lse, causal, scale=None, m
 def _flash_decode(q, k, v, scale=None):
     """Single-query attention (q is (B, H, 1, E)) over a contiguous KV cache: (out, lse)."""
     dims = _attention_dims(q, k, v)
-    dev, dtype = _check_device(q, k, v)
     B, H, _, L, _, E = dims
     if L != 1:
         raise ValueError("flash attention decode takes q_len == 1")
+    dev, dtype = _check_device(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     out = torch.empty((B, H, 1, E), dtype=dtype, device=dev)
     lse = torch.empty((B, H, 1), dtype=torch.float32, device=dev)

@@ -1,0 +1,115 @@
+"""The C ABI on a machine without a GPU: the library loads, exports every function the header
+declares, agrees with the header on the descriptor layout, and rejects bad arguments with the
+reference's messages (src/lib.rs:555-607, 658-663) before any kernel is launched."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from densecore_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dc_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(dc_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    L = _lib.lib()
+    declared = header_functions()
+    assert declared, "no functions parsed from the header"
+    assert set(declared) == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (dc_[a-z_0-9]+)$", out, re.M))
+    assert set(declared) <= exported
+
+
+def test_descriptor_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "dc_attn.h"\n'
+                   "int main(void){printf(\"%zu %zu %zu %zu %zu\\n\", sizeof(dc_attn_desc),"
+                   " offsetof(dc_attn_desc, causal), offsetof(dc_attn_desc, scale),"
+                   " offsetof(dc_attn_desc, dtype), offsetof(dc_attn_desc, mask_stride_l));"
+                   "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True,
+                                       check=True).stdout.split()))
+    D = _lib.Desc
+    assert got == [ctypes.sizeof(D), D.causal.offset, D.scale.offset, D.dtype.offset,
+                   D.mask_stride_l.offset]
+
+
+def desc(**kw):
+    d = dict(batch=2, heads=4, kv_heads=2, q_len=8, kv_len=8, head_dim=16, causal=0, has_scale=0,
+             scale=0.0, dtype=_lib.DC_F32, reserved=0, mask_stride_b=0, mask_stride_h=0,
+             mask_stride_l=0)
+    d.update(kw)
+    return _lib.Desc(**d)
+
+
+def fwd(d, mask=None):
+    L = _lib.lib()
+    return L.dc_sdpa_fwd(ctypes.byref(d), None, None, None, mask, None, None, None, 0, None)
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(kv_heads=3), _lib.DC_INVALID_ARGUMENT, "q/k/v shapes do not match"),
+    (dict(kv_heads=0), _lib.DC_INVALID_ARGUMENT, "q/k/v shapes do not match"),
+    (dict(q_len=-1), _lib.DC_INVALID_ARGUMENT, r"takes \(B, H, L, E\) tensors"),
+    (dict(dtype=7), _lib.DC_INVALID_ARGUMENT, "dtype"),
+    (dict(head_dim=300), _lib.DC_UNSUPPORTED, "head_dim"),
+    (dict(q_len=2**31), _lib.DC_UNSUPPORTED, "2\\^31"),
+])
+def test_forward_argument_errors(kw, status, msg):
+    assert fwd(desc(**kw)) == status
+    assert re.search(msg, _lib.lib().dc_last_error().decode())
+    with pytest.raises(ValueError if status == _lib.DC_INVALID_ARGUMENT else NotImplementedError,
+                       match=msg):
+        _lib.check(status)
+
+
+def test_null_pointers_rejected_and_empty_accepted():
+    assert fwd(desc()) == _lib.DC_INVALID_ARGUMENT
+    assert "null pointer" in _lib.lib().dc_last_error().decode()
+    assert fwd(desc(batch=0)) == _lib.DC_OK  # nothing to do: no launch, no pointers needed
+    assert fwd(desc(q_len=0)) == _lib.DC_OK
+
+
+def test_mask_strides_and_workspace_checks():
+    L = _lib.lib()
+    d = desc(mask_stride_b=-1)
+    assert fwd(d, mask=ctypes.c_void_p(16)) == _lib.DC_INVALID_ARGUMENT
+    assert "mask must be (B, H, L, S)" in L.dc_last_error().decode()
+    d = desc()
+    need = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
+    assert need >= 2 * 4 * 8 * 4  # dsum, float32 per (b, h, l)
+    st = L.dc_sdpa_bwd(ctypes.byref(d), *([None] * 11), need - 1, None)
+    assert st == _lib.DC_INVALID_ARGUMENT and "workspace" in L.dc_last_error().decode()
+    bf = desc(dtype=_lib.DC_BF16)
+    assert L.dc_sdpa_bwd_workspace_size(ctypes.byref(bf)) > need  # + float32 dq accumulator
+    dd = desc(q_len=2)
+    st = L.dc_sdpa_decode(ctypes.byref(dd), *([None] * 6), 1 << 20, None)
+    assert st == _lib.DC_INVALID_ARGUMENT and "q_len == 1" in L.dc_last_error().decode()
+    dc = desc(q_len=1, causal=1)
+    st = L.dc_sdpa_decode(ctypes.byref(dc), *([None] * 6), 1 << 20, None)
+    assert st == _lib.DC_INVALID_ARGUMENT and "non-causal" in L.dc_last_error().decode()
+
+
+def test_decode_workspace_covers_splits():
+    L = _lib.lib()
+    for B, H, S, E in [(32, 32, 4096, 128), (1, 1, 1, 64), (1, 1, 100000, 64), (4, 8, 0, 32)]:
+        d = desc(batch=B, heads=H, kv_heads=H, q_len=1, kv_len=S, head_dim=E)
+        ws = L.dc_sdpa_decode_workspace_size(ctypes.byref(d))
+        # at least one (acc[E], max, sum) record per (batch, head), and no more than 2048 keys
+        # per split
+        splits = max(1, -(-S // 2048))
+        assert ws >= B * H * splits * (E + 2) * 4

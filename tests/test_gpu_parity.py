@@ -175,3 +175,27 @@ def test_errors_match_reference():
     out, lse = _native._flash_attention(x, x, x, False)
     with pytest.raises(ValueError, match="backward shapes do not match"):
         _native._flash_attention_backward(out, x, x, x, out, lse[..., :2], False)
+
+
+def _golden_tags():
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "sdpa_golden.npz"))
+    return z, sorted({k.split("/")[0] for k in z.files if not k.startswith("in_")})
+
+
+@pytest.mark.parametrize("tag", _golden_tags()[1])
+def test_golden_fixtures(tag):
+    """The committed fixtures (tests/golden/sdpa_golden.npz), no live oracle involved."""
+    z, _ = _golden_tags()
+    src = str(z[f"{tag}/inputs"])
+    q, k, v, g = (z[f"{src}/{n}"] for n in "qkvg")
+    causal, scale = z[f"{tag}/meta"]
+    scale = None if np.isnan(scale) else float(scale)
+    mask = z[f"{tag}/mask"] if f"{tag}/mask" in z.files else None
+    print(f"[case] golden {tag}", flush=True)
+    out, lse = _run_fwd(q, k, v, bool(causal), scale, mask)
+    assert_f32(out, z[f"{tag}/out"], f"{tag} out")
+    assert_f32(lse, z[f"{tag}/lse"], f"{tag} lse")
+    got = _run_bwd(g, q, k, v, z[f"{tag}/out"], z[f"{tag}/lse"], bool(causal), scale, mask)
+    for name, a in zip(("dq", "dk", "dv"), got):
+        assert_f32(a, z[f"{tag}/{name}"], f"{tag} {name}")
