@@ -15,6 +15,7 @@
 //     LDS tile, multiplies by its K rows (also kept in LDS) and adds the 32 x D partial into a
 //     float32 dQ accumulator with coalesced global atomics.
 // A small pre-kernel computes dsum and clears the dQ accumulator.
+#include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
 
@@ -31,29 +32,10 @@ struct BwdSmem {
     float k[kBN][D + 4];
     float q[kBM][D + 4];
     float dout[kBM][D + 4];
-    float lse2[kBM];
+    float lse[kBM];
     float dsum[kBM];
     float ds[kWaves][32][36];
 };
-
-// dsum[row] = sum_d dO[row][d] * O[row][d]; also clears the float32 dQ accumulator row.
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
-    const AttnShape &s = a.s;
-    const int64_t rows = (int64_t)s.B * s.H * s.L;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int part = threadIdx.x & 15;
-    if (row >= rows) return;  // whole 16-lane groups exit together
-    const T *go = static_cast<const T *>(a.dout) + row * s.E;
-    const T *o = static_cast<const T *>(a.out) + row * s.E;
-    float acc = 0.f;
-    for (int d = part; d < s.E; d += 16) acc = fmaf(to_f32<T>(go[d]), to_f32<T>(o[d]), acc);
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (part == 0) a.dsum[row] = acc;
-    float *dq = a.dq_acc + row * s.E;
-    for (int d = part; d < s.E; d += 16) dq[d] = 0.f;
-}
 
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
@@ -127,7 +109,7 @@ __global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
             }
             if (tid < kBM) {
                 const int qq = m0 + tid;
-                sm.lse2[tid] = qq < s.L ? a.lse[(int64_t)bh * s.L + qq] * kLog2e : INFINITY;
+                sm.lse[tid] = qq < s.L ? a.lse[(int64_t)bh * s.L + qq] : INFINITY;
                 sm.dsum[tid] = qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
             }
             __syncthreads();
@@ -155,14 +137,11 @@ __global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int qrow = acc_row(r, g), qq = m0 + qrow;
-                float x;
-                if (MASK) {
-                    const float mv = (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-                    x = (sacc[r] * s.scale + mv) * kLog2e;
-                } else {
-                    x = sacc[r] * s.scale_log2;
-                }
-                float p = exp2_fast(x - sm.lse2[qrow]);
+                // scale * q.k (+ mask) - lse in natural-log units, as the reference forms it,
+                // then one conversion to base 2 for v_exp_f32.
+                float x = sacc[r] * s.scale;
+                if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+                float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
                 if (key >= s.S || (CAUSAL && key > qq)) p = 0.f;
                 sacc[r] = p;
                 pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
@@ -249,14 +228,14 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
     const dim3 grid(nkt * a.s.B * a.s.Hkv), block(kThreads);
     const bool mask = a.s.mask != nullptr;
     if (a.s.causal && mask)
-        hipLaunchKernelGGL((bwd_f32_kernel<D, true, true>), grid, block, 0, st, a);
+        return_if(launch(bwd_f32_kernel<D, true, true>, grid, block, st, a));
     else if (a.s.causal)
-        hipLaunchKernelGGL((bwd_f32_kernel<D, true, false>), grid, block, 0, st, a);
+        return_if(launch(bwd_f32_kernel<D, true, false>, grid, block, st, a));
     else if (mask)
-        hipLaunchKernelGGL((bwd_f32_kernel<D, false, true>), grid, block, 0, st, a);
+        return_if(launch(bwd_f32_kernel<D, false, true>, grid, block, st, a));
     else
-        hipLaunchKernelGGL((bwd_f32_kernel<D, false, false>), grid, block, 0, st, a);
-    return hipGetLastError();
+        return_if(launch(bwd_f32_kernel<D, false, false>, grid, block, st, a));
+    return hipSuccess;
 }
 
 }  // namespace
@@ -264,9 +243,7 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st) {
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
     if (rows > 0) {
-        hipLaunchKernelGGL((bwd_pre_kernel<float>), dim3((rows + 15) / 16), dim3(256), 0, st, a);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        return_if(launch(bwd_pre_kernel<float>, dim3((rows + 15) / 16), dim3(256), st, a));
     }
     if (a.s.B * a.s.Hkv == 0 || a.s.S == 0) return hipSuccess;
     if (a.s.E <= 32) return launch_d<32>(a, st);

@@ -49,11 +49,37 @@ DEVI float xor32_add(float x) { return x + __shfl_xor(x, 32, 64); }
 DEVI float bf16_to_f32(__bf16 x) { return static_cast<float>(x); }
 DEVI __bf16 f32_to_bf16(float x) { return static_cast<__bf16>(x); }  // round to nearest even
 
+// x[at + j] (j = 0..7) as hi + lo with hi = bf16(x) and lo = bf16(x - hi).
+DEVI void split_bf16(const f32x16 &x, int at, bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 h = static_cast<__bf16>(x[at + j]);
+        hi[j] = h;
+        lo[j] = static_cast<__bf16>(x[at + j] - static_cast<float>(h));
+    }
+}
+
 template <typename T> DEVI float to_f32(T x);
 template <> DEVI float to_f32<float>(float x) { return x; }
 template <> DEVI float to_f32<__bf16>(__bf16 x) { return static_cast<float>(x); }
 template <typename T> DEVI T from_f32(float x);
 template <> DEVI float from_f32<float>(float x) { return x; }
 template <> DEVI __bf16 from_f32<__bf16>(float x) { return static_cast<__bf16>(x); }
+
+// Launches `kernel` and returns the status of this launch alone (hipGetLastError would also
+// report errors left behind by unrelated earlier calls in the process).
+template <typename... Params, typename... Args>
+inline hipError_t launch(void (*kernel)(Params...), dim3 grid, dim3 block, hipStream_t stream,
+                         Args... args) {
+    static_assert(sizeof...(Params) == sizeof...(Args), "argument count");
+    void *ptrs[] = {static_cast<void *>(&args)...};
+    return hipLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, 0, stream);
+}
+
+#define return_if(expr)                      \
+    do {                                     \
+        const hipError_t err_ = (expr);      \
+        if (err_ != hipSuccess) return err_; \
+    } while (0)
 
 }  // namespace dc

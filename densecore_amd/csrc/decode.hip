@@ -194,10 +194,9 @@ hipError_t launch_t(const DecodeArgs &args, hipStream_t st) {
     DecodeArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;
     const int BH = a.s.B * a.s.H;
-    hipLaunchKernelGGL((decode_split_kernel<T, D>), dim3((int64_t)a.splits * BH), dim3(kThreads), 0,
-                       st, a);
-    hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(BH), dim3(64), 0, st, a);
-    return hipGetLastError();
+    return_if(launch(decode_split_kernel<T, D>, dim3((int64_t)a.splits * BH), dim3(kThreads), st, a));
+    return_if(launch(decode_merge_kernel<T>, dim3(BH), dim3(64), st, a));
+    return hipSuccess;
 }
 
 template <typename T>

@@ -250,14 +250,14 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
     const bool mask = a.s.mask != nullptr;
     if (a.s.causal && mask)
-        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, true, true>), grid, block, 0, st, a);
+        return_if(launch(fwd_f32_kernel<D, BN, true, true>, grid, block, st, a));
     else if (a.s.causal)
-        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, true, false>), grid, block, 0, st, a);
+        return_if(launch(fwd_f32_kernel<D, BN, true, false>, grid, block, st, a));
     else if (mask)
-        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, false, true>), grid, block, 0, st, a);
+        return_if(launch(fwd_f32_kernel<D, BN, false, true>, grid, block, st, a));
     else
-        hipLaunchKernelGGL((fwd_f32_kernel<D, BN, false, false>), grid, block, 0, st, a);
-    return hipGetLastError();
+        return_if(launch(fwd_f32_kernel<D, BN, false, false>, grid, block, st, a));
+    return hipSuccess;
 }
 
 }  // namespace

@@ -1,0 +1,131 @@
+"""GPU parity of the bfloat16 kernels (fp32 accumulation) against the float32 oracle run on
+the exact float32 upcast of the same bf16 inputs.
+
+Tolerance (the target's for bf16): |gpu - ref| <= 1e-2 |ref| + 1e-2 rms(ref), elementwise.
+
+Each function is compared on identical inputs.  The backward takes (out, lse) as inputs, so
+the oracle's backward is given the GPU forward's bf16 out (upcast) and lse: dsum = rowsum(dO *
+out) formed from a bf16-rounded out differs from one formed from a float32 out by about
+2^-9 |dO| |out|, which alone can exceed the elementwise bound for small gradients.
+
+C5 (B2 H32 T8192 D128, causal) runs at full size on the GPU; the oracle checks it through
+causal row windows, which is exact: query rows [a, b) of a causal problem depend only on keys
+[0, b), so the oracle on (q[a:b], k[:b], v[:b]) with the mask "key <= row + a" gives those
+rows' out, lse and dq; with b = T it also gives dk and dv of every key >= a."""
+import numpy as np
+import pytest
+
+from tests._data import assert_bf16, bf16_round, make_inputs
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _bf(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV).to(torch.bfloat16)
+
+
+def _np(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def _offset_causal(rows, keys, a):
+    allowed = np.arange(keys)[None, :] <= np.arange(rows)[:, None] + a
+    return np.where(allowed, np.float32(0), np.float32(-np.inf))
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,E,causal", [
+    (2, 2, 2, 7, 7, 5, False), (1, 3, 3, 33, 33, 16, True), (1, 2, 2, 100, 37, 12, False),
+    (1, 1, 1, 200, 200, 64, True), (2, 4, 2, 300, 300, 128, True), (1, 2, 1, 129, 257, 128, False),
+    (1, 2, 2, 64, 64, 32, True), (2, 2, 2, 190, 190, 100, True),
+])
+def test_bf16_shapes(oracle_lib, B, H, Hkv, L, S, E, causal):
+    from densecore_amd import _native
+    rng = np.random.default_rng(L * 7 + S + E)
+    q, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(2))
+    k, v = (bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32)) for _ in range(2))
+    print(f"[case] bf16 B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
+    out, lse = _native._flash_attention(tq, tk, tv, causal)
+    assert out.dtype == torch.bfloat16 and lse.dtype == torch.float32
+    assert_bf16(_np(out), ref_o, "out")
+    assert_bf16(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), causal)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, causal)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert a.dtype == torch.bfloat16
+        assert_bf16(_np(a), b, name)
+
+
+def test_bf16_masked(oracle_lib):
+    from densecore_amd import _native
+    rng = np.random.default_rng(77)
+    B, H, L, S, E = 2, 3, 150, 170, 64
+    q, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(2))
+    k, v = (bf16_round(rng.standard_normal((B, H, S, E), dtype=np.float32)) for _ in range(2))
+    mask = np.where(rng.random((B, 1, L, S)) > 0.3, np.float32(0), np.float32(-np.inf))
+    mask[0, 0, 5, :] = -np.inf  # a fully masked row
+    full = np.ascontiguousarray(np.broadcast_to(mask, (B, H, L, S)))
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False, None, full)
+    tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
+    tm = torch.from_numpy(mask).to(DEV).expand(B, H, L, S)
+    out, lse = _native._flash_attention(tq, tk, tv, False, None, tm)
+    assert_bf16(_np(out), ref_o, "out")
+    assert_bf16(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), False, None, full)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, False, None, tm)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_bf16(_np(a), b, name)
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,E", [(4, 8, 8, 4096, 128), (2, 4, 2, 1000, 64), (1, 2, 2, 77, 100)])
+def test_bf16_decode(oracle_lib, B, H, Hkv, S, E):
+    from densecore_amd import _native
+    rng = np.random.default_rng(S)
+    q = bf16_round(rng.standard_normal((B, H, 1, E), dtype=np.float32))
+    k, v = (bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32) * 0.5) for _ in range(2))
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False)
+    out, lse = _native._flash_decode(_bf(q), _bf(k), _bf(v))
+    assert_bf16(_np(out), ref_o, "decode out")
+    assert_bf16(_np(lse), ref_l, "decode lse")
+
+
+@pytest.fixture(scope="module")
+def c5_run():
+    """Full C5 forward + backward on the GPU, kept on the host for the window checks."""
+    from densecore_amd import _native
+    d = make_inputs("C5")
+    print("[case] C5 full forward+backward (B2 H32 T8192 D128 bf16)", flush=True)
+    tq, tk, tv, tg = (_bf(d[n]) for n in "qkvg")
+    out, lse = _native._flash_attention(tq, tk, tv, True)
+    dq, dk, dv = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, True)
+    res = {n: _np(x) for n, x in (("out", out), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv))}
+    for n, x in res.items():
+        assert np.isfinite(x).all(), n
+    return d, res
+
+
+HEADS = [(0, 0), (1, 17)]
+
+
+@pytest.mark.parametrize("a,b", [(0, 1024), (4096, 4224), (7168, 8192)])
+def test_c5_windows(oracle_lib, c5_run, a, b):
+    d, res = c5_run
+    sel = lambda x, rows: np.stack([x[bi, hi, rows] for bi, hi in HEADS])[None]  # (1, 2, n, E)
+    q, g = sel(d["q"], slice(a, b)), sel(d["g"], slice(a, b))
+    k, v = sel(d["k"], slice(0, b)), sel(d["v"], slice(0, b))
+    mask = np.ascontiguousarray(np.broadcast_to(_offset_causal(b - a, b, a), (1, 2, b - a, b)))
+    print(f"[case] C5 window rows [{a}, {b})", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False, None, mask)
+    assert_bf16(sel(res["out"], slice(a, b)), ref_o, f"C5 out[{a}:{b}]")
+    assert_bf16(sel(res["lse"][..., None], slice(a, b))[..., 0], ref_l, f"C5 lse[{a}:{b}]")
+    go, gl = sel(res["out"], slice(a, b)), sel(res["lse"][..., None], slice(a, b))[..., 0]
+    rq, rk, rv = oracle_lib.backward(g, q, k, v, go, gl, False, None, mask)
+    assert_bf16(sel(res["dq"], slice(a, b)), rq, f"C5 dq[{a}:{b}]")
+    if b == d["q"].shape[2]:
+        assert_bf16(sel(res["dk"], slice(a, b)), rk[:, :, a:], f"C5 dk[{a}:]")
+        assert_bf16(sel(res["dv"], slice(a, b)), rv[:, :, a:], f"C5 dv[{a}:]")
