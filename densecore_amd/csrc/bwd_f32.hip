@@ -11,9 +11,12 @@
 //   * each step stages a 32-query tile of Q and dO (plus lse and dsum) in LDS;
 //   * S and dP are computed with queries as rows and this wave's keys as columns, so P and dS
 //     feed dV^T += dO^T P and dK^T += Q^T dS directly from the accumulators;
-//   * dQ needs dS with queries on lanes: each wave bounces its 32x32 dS tile through a private
-//     LDS tile, multiplies by its K rows (also kept in LDS) and adds the 32 x D partial into a
-//     float32 dQ accumulator with coalesced global atomics.
+//   * the next step's Q, dO, lse and dsum are loaded into registers while a step computes;
+//   * dQ needs dS with queries on lanes: the four waves write their dS into one shared 32 x 128
+//     LDS tile, and after the next barrier each wave multiplies its share of it by the K tile
+//     (kept in LDS) into disjoint 16 x 16 blocks of dQ, which go to the float32 dQ
+//     accumulator with one coalesced global atomic per element and workgroup step.  That
+//     product runs between the next step's two barriers, so it costs no barrier of its own.
 // A small pre-kernel computes dsum and clears the dQ accumulator.
 #include "bwd_common.hpp"
 #include "common.hpp"
@@ -29,16 +32,107 @@ constexpr int kBM = 32;           // queries per step
 
 template <int D>
 struct BwdSmem {
-    float k[kBN][D + 4];
-    float q[kBM][D + 4];
+    // K rows, read by the dQ product with lanes along d and four keys per step: a row stride
+    // of D + 16 words puts the four key rows of one read in different 16-bank windows.
+    float k[kBN][D + 16];
+    float q[kBM][D + 4];         // read along d with ds_read_b128 per lane: padded rows
     float dout[kBM][D + 4];
+    float ds[kBM][kBN + 4];      // dS of the step, all four waves' keys
     float lse[kBM];
     float dsum[kBM];
-    float ds[kWaves][32][36];
 };
 
+// Register staging of one step's Q and dO rows (fast path: E == D, 16-byte aligned).
+template <int D>
+struct QStage {
+    static constexpr int C4 = D / 4;
+    static constexpr int N = kBM * C4 / kThreads;
+    static_assert(kBM * C4 % kThreads == 0, "tile must split evenly over the workgroup");
+    f32x4 q[N], o[N];
+    float lse, dsum;
+
+    DEVI void load(const float *qb, const float *gb, const float *lseb, const float *dsumb, int m0,
+                   int L, int tid) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4, qq = m0 + r;
+            if (qq < L) {
+                q[j] = *reinterpret_cast<const f32x4 *>(qb + (int64_t)qq * D + c);
+                o[j] = *reinterpret_cast<const f32x4 *>(gb + (int64_t)qq * D + c);
+            } else {
+                q[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (tid < kBM) {
+            const int qq = m0 + tid;
+            lse = qq < L ? lseb[qq] : INFINITY;
+            dsum = qq < L ? dsumb[qq] : 0.f;
+        }
+    }
+    DEVI void store(BwdSmem<D> &sm, int tid) const {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4;
+            *reinterpret_cast<f32x4 *>(&sm.q[r][c]) = q[j];
+            *reinterpret_cast<f32x4 *>(&sm.dout[r][c]) = o[j];
+        }
+        if (tid < kBM) sm.lse[tid] = lse, sm.dsum[tid] = dsum;
+    }
+};
+
+// Generic path (any E <= D, any alignment): straight into LDS.
+template <int D>
+DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const float *lseb,
+                        const float *dsumb, int m0, int L, int E, int tid) {
+    for (int i = tid; i < kBM * D; i += kThreads) {
+        const int r = i / D, c = i % D, qq = m0 + r;
+        const bool ok = qq < L && c < E;
+        sm.q[r][c] = ok ? qb[(int64_t)qq * E + c] : 0.f;
+        sm.dout[r][c] = ok ? gb[(int64_t)qq * E + c] : 0.f;
+    }
+    if (tid < kBM) {
+        const int qq = m0 + tid;
+        sm.lse[tid] = qq < L ? lseb[qq] : INFINITY;
+        sm.dsum[tid] = qq < L ? dsumb[qq] : 0.f;
+    }
+}
+
+// dQ[m0 .. m0+31][:] += scale * dS K for the step whose dS is in sm.ds.  The 32 x D tile is
+// split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32 over `nkeys` keys: lane l
+// supplies A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element
+// gets exactly one global atomic per workgroup step.
+template <int D>
+DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L, int E,
+                     float scale, int wave, int lane) {
+    constexpr int TPW = D / 32;
+    const int r16 = lane & 15, c4 = lane >> 4;
+    const int qh = wave >> 1, dbase = (wave & 1) * (D / 2);
+    f32x4 acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int steps = (nkeys + 3) / 4;
+#pragma unroll 4
+    for (int st = 0; st < steps; ++st) {
+        const float av = sm.ds[qh * 16 + r16][4 * st + c4];
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                av, sm.k[4 * st + c4][dbase + 16 * j + r16], acc[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+        const int d = dbase + 16 * j + r16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int qq = m0 + qh * 16 + 4 * c4 + v;
+            if (qq < L && d < E) unsafeAtomicAdd(dqb + (int64_t)qq * E + d, acc[j][v] * scale);
+        }
+    }
+}
+
 template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
     constexpr int DH = D / 2;
     constexpr int NDT = D / 32;
     __shared__ BwdSmem<D> sm;
@@ -78,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
             }
         }
     }
-    // The workgroup's K tile in LDS, read with lanes along the head dim by the dQ product.
+    // The workgroup's K tile in LDS, for the dQ product.
     for (int i = tid; i < kBN * D; i += kThreads) {
         const int r = i / D, c = i % D, kk = n0 + r;
         sm.k[r][c] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
@@ -90,108 +184,100 @@ __global__ __launch_bounds__(kThreads) void bwd_f32_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[dt][r] = 0.f, dv[dt][r] = 0.f;
 
+    // Steps run over (query head of this kv head, 32-query tile); causal skips the tiles
+    // that end before this workgroup's first key.
     const int m_begin = CAUSAL ? (n0 / kBM) * kBM : 0;
-    for (int rep = 0; rep < s.repeat; ++rep) {
-        const int h = hk * s.repeat + rep;
-        const int bh = b * s.H + h;
-        const float *qb = static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E;
-        const float *gb = static_cast<const float *>(a.dout) + (int64_t)bh * s.L * s.E;
+    const int per_head = s.L > m_begin ? (s.L - m_begin + kBM - 1) / kBM : 0;
+    const int nsteps = per_head * s.repeat;
+    const int key_end = min(kBN, s.S - n0);  // keys of this tile that exist
+    auto step_head = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
+    auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kBM; };
+    // Keys of the tile a step's dQ product must cover (causal: up to the step's last query).
+    auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
+
+    QStage<D> stage;
+    if (s.vec && nsteps > 0) {
+        const int bh = step_head(0);
+        stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
+                   static_cast<const float *>(a.dout) + (int64_t)bh * s.L * D,
+                   a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, step_m0(0), s.L, tid);
+    }
+    int prev_bh = -1, prev_m0 = 0;
+    for (int i = 0; i < nsteps; ++i) {
+        const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
+        __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
+        if (prev_bh >= 0)
+            dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0),
+                          s.L, s.E, s.scale, wave, lane);
+        if (s.vec) {
+            stage.store(sm, tid);
+        } else {
+            stage_generic<D>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
+                             static_cast<const float *>(a.dout) + (int64_t)bh * s.L * s.E,
+                             a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
+        }
+        __syncthreads();  // the tile is staged and the previous dQ product has read sm.ds
+        if (s.vec && i + 1 < nsteps) {
+            const int nbh = step_head(i + 1);
+            stage.load(static_cast<const float *>(a.q) + (int64_t)nbh * s.L * D,
+                       static_cast<const float *>(a.dout) + (int64_t)nbh * s.L * D,
+                       a.lse + (int64_t)nbh * s.L, a.dsum + (int64_t)nbh * s.L, step_m0(i + 1),
+                       s.L, tid);
+        }
+        prev_bh = bh, prev_m0 = m0;
+
+        // A wave has work if some query of the tile sees one of its keys; keys the dQ product
+        // will read but no query sees are never read (step_keys stops before them).
+        const bool live = kw0 < s.S && (!CAUSAL || m0 + kBM - 1 >= kw0);
+        if (!live) continue;
         const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
-        float *dqb = a.dq_acc + (int64_t)bh * s.L * s.E;
 
-        for (int m0 = m_begin; m0 < s.L; m0 += kBM) {
-            __syncthreads();  // previous step's readers are done
-            for (int i = tid; i < kBM * D; i += kThreads) {
-                const int r = i / D, c = i % D, qq = m0 + r;
-                const bool ok = qq < s.L && c < s.E;
-                sm.q[r][c] = ok ? qb[(int64_t)qq * s.E + c] : 0.f;
-                sm.dout[r][c] = ok ? gb[(int64_t)qq * s.E + c] : 0.f;
-            }
-            if (tid < kBM) {
-                const int qq = m0 + tid;
-                sm.lse[tid] = qq < s.L ? a.lse[(int64_t)bh * s.L + qq] : INFINITY;
-                sm.dsum[tid] = qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
-            }
-            __syncthreads();
-
-            // A wave has work if some query of the tile sees one of its keys.
-            const bool live = kw0 < s.S && (!CAUSAL || m0 + kBM - 1 >= kw0);
-            if (!live) continue;
-
-            // S = Q K^T and dP = dO V^T: rows are queries, columns are this wave's keys.
-            f32x16 sacc, pacc;
+        // S = Q K^T and dP = dO V^T: rows are queries, columns are this wave's keys.
+        f32x16 sacc, pacc;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
 #pragma unroll
-            for (int t4 = 0; t4 < DH; t4 += 4) {
-                const f32x4 qq = *reinterpret_cast<const f32x4 *>(&sm.q[lr][g * DH + t4]);
-                const f32x4 oo = *reinterpret_cast<const f32x4 *>(&sm.dout[lr][g * DH + t4]);
+        for (int t4 = 0; t4 < DH; t4 += 4) {
+            const f32x4 qq = *reinterpret_cast<const f32x4 *>(&sm.q[lr][g * DH + t4]);
+            const f32x4 oo = *reinterpret_cast<const f32x4 *>(&sm.dout[lr][g * DH + t4]);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    sacc = mfma_f32(qq[u], kreg[t4 + u], sacc);
-                    pacc = mfma_f32(oo[u], vreg[t4 + u], pacc);
-                }
+            for (int u = 0; u < 4; ++u) {
+                sacc = mfma_f32(qq[u], kreg[t4 + u], sacc);
+                pacc = mfma_f32(oo[u], vreg[t4 + u], pacc);
             }
+            if (t4 % 8 == 4) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
+        }
 
-            // P and dS, elementwise in the accumulator layout.
+        // P and dS, elementwise in the accumulator layout; dS goes to the shared tile.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int qrow = acc_row(r, g), qq = m0 + qrow;
+            // scale * q.k (+ mask) - lse in natural-log units, as the reference forms it,
+            // then one conversion to base 2 for v_exp_f32.
+            float x = sacc[r] * s.scale;
+            if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+            float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
+            if (key >= s.S || (CAUSAL && key > qq)) p = 0.f;
+            sacc[r] = p;
+            pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
+            sm.ds[qrow][wave * 32 + lr] = pacc[r];
+        }
+
+        // dV^T += dO^T P and dK^T += Q^T dS (reduction over this tile's queries).
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int qrow = acc_row(r, g), qq = m0 + qrow;
-                // scale * q.k (+ mask) - lse in natural-log units, as the reference forms it,
-                // then one conversion to base 2 for v_exp_f32.
-                float x = sacc[r] * s.scale;
-                if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-                float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
-                if (key >= s.S || (CAUSAL && key > qq)) p = 0.f;
-                sacc[r] = p;
-                pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
+                const int qrow = acc_row(r, g);
+                dv[dt] = mfma_f32(sm.dout[qrow][dt * 32 + lr], sacc[r], dv[dt]);
+                dk[dt] = mfma_f32(sm.q[qrow][dt * 32 + lr], pacc[r], dk[dt]);
+                if (r % 4 == 3) __builtin_amdgcn_sched_barrier(0);
             }
-
-            // dV^T += dO^T P and dK^T += Q^T dS (reduction over this tile's queries).
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int qrow = acc_row(r, g);
-                    dv[dt] = mfma_f32(sm.dout[qrow][dt * 32 + lr], sacc[r], dv[dt]);
-                    dk[dt] = mfma_f32(sm.q[qrow][dt * 32 + lr], pacc[r], dk[dt]);
-                }
-
-            // dQ (queries x D) += dS K over this wave's 32 keys, via a private LDS transpose.
-            float(*ds)[36] = sm.ds[wave];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ds[acc_row(r, g)][lr] = pacc[r];
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
-            __builtin_amdgcn_wave_barrier();
-            f32x16 dq[NDT];
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
-#pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4) {
-                const f32x4 dsv = *reinterpret_cast<const f32x4 *>(&ds[lr][8 * s4 + 4 * g]);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int kk = wave * 32 + 8 * s4 + 4 * g + u;
-#pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt)
-                        dq[dt] = mfma_f32(dsv[u], sm.k[kk][dt * 32 + lr], dq[dt]);
-                }
-            }
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const int d = dt * 32 + lr;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int qq = m0 + acc_row(r, g);
-                    if (qq < s.L && d < s.E)
-                        unsafeAtomicAdd(dqb + (int64_t)qq * s.E + d, dq[dt][r] * s.scale);
-                }
-            }
-        }
     }
+    __syncthreads();
+    if (prev_bh >= 0)
+        dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0), s.L,
+                      s.E, s.scale, wave, lane);
 
     // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
     if (key < s.S) {

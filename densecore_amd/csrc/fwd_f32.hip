@@ -75,7 +75,7 @@ DEVI void load_kv_generic(FwdSmem<D, BN> &sm, const float *kb, const float *vb, 
 }
 
 template <int D, int BN, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kThreads) void fwd_f32_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
     constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
     __shared__ FwdSmem<D, BN> sm;
