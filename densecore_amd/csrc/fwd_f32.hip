@@ -81,7 +81,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     __shared__ FwdSmem<D, BN> sm;
 
     const AttnShape &s = a.s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches stay scalar
     const int BH = s.B * s.H;
     const int nqt = (s.L + kBM - 1) / kBM;
     const int bid = blockIdx.x;
@@ -140,11 +141,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         __syncthreads();
         if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
 
-        // Which 32-key sub-tiles have any key visible to this wave's queries.
+        // Which 32-key sub-tiles have any key visible to this wave's queries (a prefix of
+        // them), and whether any key of the tile needs masking for this wave (causal diagonal,
+        // end of the sequence).  Both are wave-uniform.
         bool live[NT];
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
             live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
+        if (!live[0]) continue;  // nothing visible: the next barrier is at the loop top
+        const bool edge = n0 + BN > s.S || (CAUSAL && n0 + BN - 1 > wave_last_q - 31);
 
         // S^T = K Q^T: rows are keys, columns are this wave's 32 queries.
         f32x16 sacc[NT];
@@ -165,25 +170,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             }
         }
 
-        // Scores in log2 units, masked; tile max per query.
-        float mx = -INFINITY;
+        // Scores in log2 units (masked on edge tiles); tile max per query.
 #pragma unroll
-        for (int kt = 0; kt < NT; ++kt) {
+        for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int key = n0 + kt * 32 + acc_row(r, g);
-                float x;
                 if (MASK) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
                     const float mv = (key < s.S && qi < s.L) ? mrow[key] : 0.f;
-                    x = (sacc[kt][r] * s.scale + mv) * kLog2e;
+                    sacc[kt][r] = (sacc[kt][r] * s.scale + mv) * kLog2e;
                 } else {
-                    x = sacc[kt][r] * s.scale_log2;
+                    sacc[kt][r] *= s.scale_log2;
                 }
-                if (key >= s.S || (CAUSAL && key > qi) || !live[kt]) x = -INFINITY;
-                sacc[kt][r] = x;
-                mx = fmaxf(mx, x);
             }
+        if (edge) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
+                    if (key >= s.S || (CAUSAL && key > qi) || !live[kt]) sacc[kt][r] = -INFINITY;
+                }
         }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
         mx = xor32_max(mx);
         const float m_new = fmaxf(m_run, mx);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
