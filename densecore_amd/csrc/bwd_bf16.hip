@@ -81,7 +81,8 @@ __global__ __launch_bounds__(kThreads) void bwd_bf16_kernel(BwdArgs a) {
     __shared__ BwdSmemBf16<D> sm;
 
     const AttnShape &s = a.s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches stay scalar
     const int BHk = s.B * s.Hkv;
     const int bid = blockIdx.x;
     const int ktile = bid / BHk;

@@ -248,7 +248,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             if (t4 % 8 == 4) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
         }
 
-        // P and dS, elementwise in the accumulator layout; dS goes to the shared tile.
+        // P and dS, elementwise in the accumulator layout; dS goes to the shared tile.  Keys
+        // past the end or (causal) past a query only occur when the wave's keys reach the end
+        // of the sequence or cross the diagonal of this query tile.
+        const bool edge = kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > m0);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int qrow = acc_row(r, g), qq = m0 + qrow;
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             float x = sacc[r] * s.scale;
             if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
             float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
-            if (key >= s.S || (CAUSAL && key > qq)) p = 0.f;
+            if (edge && (key >= s.S || (CAUSAL && key > qq))) p = 0.f;
             sacc[r] = p;
             pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
             sm.ds[qrow][wave * 32 + lr] = pacc[r];

@@ -112,7 +112,8 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
     __shared__ FwdSmemBf16<D> sm;
 
     const AttnShape &s = a.s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches stay scalar
     const int BH = s.B * s.H;
     const int nqt = (s.L + kBM - 1) / kBM;
     const int bid = blockIdx.x;
