@@ -13,7 +13,9 @@
 //     8-dim block (four 16-byte rows), transposes it in registers with byte permutes and
 //     writes eight 8-byte columns, so that O^T += V^T P^T reads 4 consecutive keys per lane;
 //   * P goes from the S^T accumulator straight into the bf16 B operand (the reduction index of
-//     the MFMA is permuted to match the accumulator's row order).
+//     the MFMA is permuted to match the accumulator's row order);
+//   * the running max moves only when a tile's max exceeds it by more than 8 (base 2), so the
+//     output accumulator is rarely rescaled.
 #include "common.hpp"
 #include "params.hpp"
 
@@ -31,8 +33,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int D>
 struct FwdSmemBf16 {
     __bf16 k[kBN][D + 8];   // row stride = D/2 + 4 words: ds_read_b128 conflict-free
-    __bf16 vt[D][kBN + 4];  // row stride = 34 words: ds_read_b64 conflict-free over 32 lanes
+    // [d][key] with the two middle 4-key groups of every 16 swapped (see vt_col), so a lane's
+    // 8 keys of one MFMA step are contiguous; row stride 36 words: ds_read_b128 conflict-free.
+    __bf16 vt[D][kBN + 8];
 };
+
+// Column of 4-key group kb4 in vt: inside each 16 keys the groups are stored 0, 2, 1, 3, so that
+// the keys {4g..4g+3, 8+4g..8+4g+3} a half-wave g feeds one bf16 MFMA step sit at 8g..8g+7.
+DEVI int vt_col(int kb4) {
+    const int grp = kb4 & 3;
+    return (kb4 & ~3) * 4 + (grp == 1 ? 2 : grp == 2 ? 1 : grp) * 4;
+}
 
 // Low / high 16 bits of two dwords packed into one: (a.lo, b.lo) and (a.hi, b.hi).
 DEVI uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
@@ -98,8 +109,8 @@ struct StageBf16 {
             for (int w = 0; w < 4; ++w) {
                 const u32x2 even = {pack_lo(v[j][0][w], v[j][1][w]), pack_lo(v[j][2][w], v[j][3][w])};
                 const u32x2 odd = {pack_hi(v[j][0][w], v[j][1][w]), pack_hi(v[j][2][w], v[j][3][w])};
-                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w][kb4 * 4]) = even;
-                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w + 1][kb4 * 4]) = odd;
+                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w][vt_col(kb4)]) = even;
+                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w + 1][vt_col(kb4)]) = odd;
             }
         }
     }
@@ -175,14 +186,17 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+        // One uniform test per 32-key sub-tile, outside its MFMA chain (a test inside the chain
+        // makes the compiler copy the accumulator around every MFMA).
 #pragma unroll
-        for (int st = 0; st < KS; ++st)
+        for (int kt = 0; kt < NT; ++kt) {
+            if (!live[kt]) continue;
 #pragma unroll
-            for (int kt = 0; kt < NT; ++kt) {
-                if (!live[kt]) continue;
+            for (int st = 0; st < KS; ++st) {
                 const bf16x8 kk = *reinterpret_cast<const bf16x8 *>(&sm.k[kt * 32 + lr][16 * st + 8 * g]);
                 sacc[kt] = mfma_bf16(kk, qreg[st], sacc[kt]);
             }
+        }
 
         float mx = -INFINITY;
 #pragma unroll
@@ -202,9 +216,20 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
                 mx = fmaxf(mx, x);
             }
         mx = xor32_max(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2_fast(m_run - m_use);
+        // Lazy rescaling: the exponent reference m_run moves (and O, l are rescaled) only when
+        // some lane's tile max exceeds it by more than 8, so P <= 2^8 and most tiles skip the
+        // rescale of the accumulator; out = O / l and lse = m_run + log2(l) are unchanged.
+        if (__any(mx > m_run + 8.f)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = exp2_fast(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float ls = 0.f;
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
@@ -214,16 +239,10 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
                 sacc[kt][r] = p;
                 ls += p;
             }
-        ls = xor32_add(ls);
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        l_run += xor32_add(ls);
 
         // O^T += V^T P^T, 16 keys per MFMA: registers 8u..8u+7 of the S^T accumulator hold
-        // keys 16u + {4g..4g+3, 8+4g..8+4g+3} of the 32-key sub-tile.
+        // keys 16u + {4g..4g+3, 8+4g..8+4g+3} of the 32-key sub-tile, stored contiguously in vt.
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt) {
             if (!live[kt]) continue;
@@ -231,12 +250,10 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
             for (int u = 0; u < 2; ++u) {
                 bf16x8 ph, pl;
                 split_bf16(sacc[kt], 8 * u, ph, pl);
-                const int kc = kt * 32 + 16 * u + 4 * g;
+                const int kc = kt * 32 + 16 * u + 8 * g;
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&sm.vt[dt * 32 + lr][kc]);
-                    const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&sm.vt[dt * 32 + lr][kc + 8]);
-                    const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sm.vt[dt * 32 + lr][kc]);
                     oacc[dt] = mfma_bf16(va, ph, oacc[dt]);
                     oacc[dt] = mfma_bf16(va, pl, oacc[dt]);
                 }

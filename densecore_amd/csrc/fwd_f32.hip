@@ -157,11 +157,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+        // One uniform test per 32-key sub-tile, outside its MFMA chain.
 #pragma unroll
-        for (int t4 = 0; t4 < DH; t4 += 4) {
+        for (int kt = 0; kt < NT; ++kt) {
+            if (!live[kt]) continue;
 #pragma unroll
-            for (int kt = 0; kt < NT; ++kt) {
-                if (!live[kt]) continue;
+            for (int t4 = 0; t4 < DH; t4 += 4) {
                 const f32x4 kk = *reinterpret_cast<const f32x4 *>(&sm.k[kt * 32 + lr][g * DH + t4]);
                 sacc[kt] = mfma_f32(kk[0], qreg[t4 + 0], sacc[kt]);
                 sacc[kt] = mfma_f32(kk[1], qreg[t4 + 1], sacc[kt]);
@@ -198,9 +199,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
         mx = xor32_max(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2_fast(m_run - m_use);
+        // Lazy rescaling: the exponent reference m_run moves (and O, l are rescaled) only when
+        // some lane's tile max exceeds it by more than 8, so P <= 2^8 and most tiles skip the
+        // rescale of the accumulator; out = O / l and lse = m_run + log2(l) are unchanged.
+        if (__any(mx > m_run + 8.f)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = exp2_fast(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float ls = 0.f;
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
@@ -210,13 +222,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
                 sacc[kt][r] = p;
                 ls += p;
             }
-        ls = xor32_add(ls);
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        l_run += xor32_add(ls);
 
         // O^T += V^T P^T: A = V[key][d] from LDS, B = P straight from the S^T accumulator.
 #pragma unroll
