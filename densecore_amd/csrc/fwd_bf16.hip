@@ -186,15 +186,24 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-        // One uniform test per 32-key sub-tile, outside its MFMA chain (a test inside the chain
-        // makes the compiler copy the accumulator around every MFMA).
+        // All sub-tiles live (every tile but the causal diagonal): the sub-tiles' independent
+        // MFMA chains are interleaved.  Otherwise one uniform test per sub-tile, outside its
+        // chain (a test inside the chain makes the compiler copy the accumulator around).
+        auto s_step = [&](int kt, int st) {
+            const bf16x8 kk = *reinterpret_cast<const bf16x8 *>(&sm.k[kt * 32 + lr][16 * st + 8 * g]);
+            sacc[kt] = mfma_bf16(kk, qreg[st], sacc[kt]);
+        };
+        if (live[NT - 1]) {
 #pragma unroll
-        for (int kt = 0; kt < NT; ++kt) {
-            if (!live[kt]) continue;
+            for (int st = 0; st < KS; ++st)
 #pragma unroll
-            for (int st = 0; st < KS; ++st) {
-                const bf16x8 kk = *reinterpret_cast<const bf16x8 *>(&sm.k[kt * 32 + lr][16 * st + 8 * g]);
-                sacc[kt] = mfma_bf16(kk, qreg[st], sacc[kt]);
+                for (int kt = 0; kt < NT; ++kt) s_step(kt, st);
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                if (!live[kt]) continue;
+#pragma unroll
+                for (int st = 0; st < KS; ++st) s_step(kt, st);
             }
         }
 

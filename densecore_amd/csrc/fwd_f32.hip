@@ -157,12 +157,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-        // One uniform test per 32-key sub-tile, outside its MFMA chain.
+        // The sub-tiles' independent MFMA chains are interleaved (measured faster here than
+        // testing liveness once per sub-tile outside its chain).
 #pragma unroll
-        for (int kt = 0; kt < NT; ++kt) {
-            if (!live[kt]) continue;
+        for (int t4 = 0; t4 < DH; t4 += 4) {
 #pragma unroll
-            for (int t4 = 0; t4 < DH; t4 += 4) {
+            for (int kt = 0; kt < NT; ++kt) {
+                if (!live[kt]) continue;
                 const f32x4 kk = *reinterpret_cast<const f32x4 *>(&sm.k[kt * 32 + lr][g * DH + t4]);
                 sacc[kt] = mfma_f32(kk[0], qreg[t4 + 0], sacc[kt]);
                 sacc[kt] = mfma_f32(kk[1], qreg[t4 + 1], sacc[kt]);
