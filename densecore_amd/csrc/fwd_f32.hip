@@ -8,13 +8,17 @@
 //   * the wave's queries stay in VGPRs as the B operand of S^T = K Q^T (keys x queries), so
 //     every lane owns one query column and the online-softmax state (max, sum) is a scalar per
 //     lane, combined with the other half-wave by one cross-lane exchange;
-//   * K and V tiles of BN keys are staged through LDS (row stride D + 4 floats, which keeps
-//     ds_read_b128 conflict-free), with the next tile's global loads in flight during compute;
+//   * K and V tiles of BN keys are staged through LDS with the next tile's loads in flight
+//     during compute: on the fast path (E == D, aligned rows, no mask) by global_load_lds into
+//     a second LDS buffer, otherwise through registers into rows padded to D + 4 floats (which
+//     keeps ds_read_b128 conflict-free);
 //   * P = exp2(S * scale * log2 e - m) never leaves registers: the S^T accumulator is fed back
 //     as the B operand of O^T += V^T P^T with the reduction index permuted to match.
 //
 // Head dims below the instantiated D are zero-padded on load; keys past S and (causal) keys
 // past the query are -inf before the softmax.
+#include <type_traits>
+
 #include "common.hpp"
 #include "params.hpp"
 
@@ -74,11 +78,64 @@ DEVI void load_kv_generic(FwdSmem<D, BN> &sm, const float *kb, const float *vb, 
     }
 }
 
-template <int D, int BN, bool CAUSAL, bool MASK>
+// Asynchronous path (E == D, 16-byte aligned rows): K and V tiles are double-buffered in LDS
+// and filled with global_load_lds_dwordx4 (lane i of a wave lands at the wave's LDS base +
+// 16 i), so no VGPRs stage them and the next tile streams in while this one is computed.  Rows
+// are unpadded and their 16-byte chunks are stored XOR-swizzled, chunk c of row r at c ^ swz(r),
+// which keeps both read patterns conflict-free: ds_read_b128 of one chunk by 16 consecutive
+// rows, and ds_read_b32 of 32 consecutive floats by rows R and R + 4 (the two half-waves).
+template <int D, int BN>
+struct alignas(16) FwdSmemAsync {  // one buffer of the pair
+    float k[BN][D];
+    float v[BN][D];
+};
+
+struct NoSmem {};
+
+template <int D>
+DEVI int swz(int row) {
+    return (row ^ ((row & 4) << 1)) & (D / 4 - 1);
+}
+
+// One global_load_lds_dwordx4: lane i's 16 bytes at `src` land at LDS `dst` + 16 i (`dst` is
+// wave-uniform).  Written as inline assembly so that the compiler's wait-count pass does not
+// treat the transfer as aliasing every later LDS read, which would make each tile wait for the
+// next tile's loads; the caller waits (vmcnt(0) + barrier) before reading a filled buffer.
+DEVI void lds_dma16(const float *src, float *dst) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src)
+                 : "memory", "m0");
+}
+
+// Issue this wave's share of tile [n0, n0 + BN) into buffer `buf` (keys past the end read a
+// valid row, S - 1; their scores are -inf, so they contribute nothing).
+template <int D, int BN>
+DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, int n0, int S,
+                     int wave, int lane) {
+    constexpr int C = D / 4;             // 16-byte chunks per row
+    constexpr int RPL = 64 / C;          // rows per wave-wide load
+    constexpr int ROWS = BN / kWaves;    // rows per wave
+    static_assert(ROWS % RPL == 0, "a wave loads whole rows");
+#pragma unroll
+    for (int j = 0; j < ROWS / RPL; ++j) {
+        const int r0 = wave * ROWS + j * RPL;
+        const int row = r0 + lane / C;
+        const int chunk = (lane % C) ^ swz<D>(row);  // logical chunk stored at this slot
+        const int64_t off = (int64_t)min(n0 + row, S - 1) * D + chunk * 4;
+        lds_dma16(kb + off, &sm.k[r0][0]);
+        lds_dma16(vb + off, &sm.v[r0][0]);
+    }
+}
+
+template <int D, int BN, bool CAUSAL, bool MASK, bool ASYNC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
     constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
-    __shared__ FwdSmem<D, BN> sm;
+    using Smem = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, FwdSmem<D, BN>>::type;
+    using Smem2 = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, NoSmem>::type;
+    __shared__ Smem sm;
+    __shared__ Smem2 sm2;  // the second buffer of the asynchronous path
 
     const AttnShape &s = a.s;
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
@@ -128,18 +185,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     const int ntiles = (kv_end + BN - 1) / BN;
 
     KVStage<D, BN> stage;
-    if (s.vec && ntiles > 0) stage.load(kb, vb, 0, s.S, tid);
+    if constexpr (ASYNC) {
+        if (ntiles > 0) issue_tile<D, BN>(sm, kb, vb, 0, s.S, wave, lane);
+    } else if (s.vec && ntiles > 0) {
+        stage.load(kb, vb, 0, s.S, tid);
+    }
 
-    for (int t = 0; t < ntiles; ++t) {
+    // One tile per call; the asynchronous path alternates two distinct LDS objects so that
+    // the compiler can see the in-flight loads never alias the tile being read.
+    auto tile = [&](int t, auto &cur, auto &nxt) {
         const int n0 = t * BN;
-        __syncthreads();  // everyone is done reading the previous tile
-        if (s.vec) {
-            stage.store(sm, tid);
+        if constexpr (ASYNC) {
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile t landed
+            __syncthreads();  // everyone's loads landed; everyone is done with tile t - 1
+            if (t + 1 < ntiles) issue_tile<D, BN>(nxt, kb, vb, n0 + BN, s.S, wave, lane);
         } else {
-            load_kv_generic<D, BN>(sm, kb, vb, n0, s.S, s.E, tid);
+            __syncthreads();  // everyone is done reading the previous tile
+            if (s.vec) {
+                stage.store(cur, tid);
+            } else {
+                load_kv_generic<D, BN>(cur, kb, vb, n0, s.S, s.E, tid);
+            }
+            __syncthreads();
+            if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
         }
-        __syncthreads();
-        if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
+        // K row kr, dims d..d+3 (d a multiple of 4), and V row vr, dim d, of the current tile.
+        auto kread = [&](int kr, int d) -> f32x4 {
+            if constexpr (ASYNC)
+                return *reinterpret_cast<const f32x4 *>(&cur.k[kr][((d >> 2) ^ swz<D>(kr)) << 2]);
+            else
+                return *reinterpret_cast<const f32x4 *>(&cur.k[kr][d]);
+        };
+        auto vread = [&](int vr, int d) -> float {
+            if constexpr (ASYNC)
+                return cur.v[vr][(((d >> 2) ^ swz<D>(vr)) << 2) | (d & 3)];
+            else
+                return cur.v[vr][d];
+        };
 
         // Which 32-key sub-tiles have any key visible to this wave's queries (a prefix of
         // them), and whether any key of the tile needs masking for this wave (causal diagonal,
@@ -148,7 +230,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
             live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
-        if (!live[0]) continue;  // nothing visible: the next barrier is at the loop top
+        if (!live[0]) return;  // nothing visible: the next barrier is at the loop top
         const bool edge = n0 + BN > s.S || (CAUSAL && n0 + BN - 1 > wave_last_q - 31);
 
         // S^T = K Q^T: rows are keys, columns are this wave's 32 queries.
@@ -164,7 +246,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) {
                 if (!live[kt]) continue;
-                const f32x4 kk = *reinterpret_cast<const f32x4 *>(&sm.k[kt * 32 + lr][g * DH + t4]);
+                const f32x4 kk = kread(kt * 32 + lr, g * DH + t4);
                 sacc[kt] = mfma_f32(kk[0], qreg[t4 + 0], sacc[kt]);
                 sacc[kt] = mfma_f32(kk[1], qreg[t4 + 1], sacc[kt]);
                 sacc[kt] = mfma_f32(kk[2], qreg[t4 + 2], sacc[kt]);
@@ -233,9 +315,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    oacc[dt] = mfma_f32(sm.v[kt * 32 + acc_row(r, g)][dt * 32 + lr], sacc[kt][r],
+                    oacc[dt] = mfma_f32(vread(kt * 32 + acc_row(r, g), dt * 32 + lr), sacc[kt][r],
                                         oacc[dt]);
         }
+    };
+    if constexpr (ASYNC) {
+        for (int t = 0; t < ntiles; t += 2) {
+            tile(t, sm, sm2);
+            if (t + 1 < ntiles) tile(t + 1, sm2, sm);
+        }
+    } else {
+        for (int t = 0; t < ntiles; ++t) tile(t, sm, sm);
     }
 
     if (qi < s.L) {
@@ -269,14 +359,20 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     const int nqt = (a.s.L + kBM - 1) / kBM;
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
     const bool mask = a.s.mask != nullptr;
-    if (a.s.causal && mask)
-        return_if(launch(fwd_f32_kernel<D, BN, true, true>, grid, block, st, a));
-    else if (a.s.causal)
-        return_if(launch(fwd_f32_kernel<D, BN, true, false>, grid, block, st, a));
-    else if (mask)
-        return_if(launch(fwd_f32_kernel<D, BN, false, true>, grid, block, st, a));
-    else
-        return_if(launch(fwd_f32_kernel<D, BN, false, false>, grid, block, st, a));
+    if (a.s.vec && !mask) {  // (the masked kernels keep register staging: fewer VGPRs)
+        if (a.s.causal)
+            return_if(launch(fwd_f32_kernel<D, BN, true, false, true>, grid, block, st, a));
+        else
+            return_if(launch(fwd_f32_kernel<D, BN, false, false, true>, grid, block, st, a));
+    } else if (a.s.causal && mask) {
+        return_if(launch(fwd_f32_kernel<D, BN, true, true, false>, grid, block, st, a));
+    } else if (a.s.causal) {
+        return_if(launch(fwd_f32_kernel<D, BN, true, false, false>, grid, block, st, a));
+    } else if (mask) {
+        return_if(launch(fwd_f32_kernel<D, BN, false, true, false>, grid, block, st, a));
+    } else {
+        return_if(launch(fwd_f32_kernel<D, BN, false, false, false>, grid, block, st, a));
+    }
     return hipSuccess;
 }
 
