@@ -9,7 +9,7 @@
 //     every lane owns one query column and the online-softmax state (max, sum) is a scalar per
 //     lane, combined with the other half-wave by one cross-lane exchange;
 //   * K and V tiles of BN keys are staged through LDS with the next tile's loads in flight
-//     during compute: on the fast path (E == D, aligned rows, no mask) by global_load_lds into
+//     during compute: on the fast path (E == D, aligned rows) by global_load_lds into
 //     a second LDS buffer, otherwise through registers into rows padded to D + 4 floats (which
 //     keeps ds_read_b128 conflict-free);
 //   * P = exp2(S * scale * log2 e - m) never leaves registers: the S^T accumulator is fed back
@@ -230,7 +230,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
             live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
-        if (!live[0]) return;  // nothing visible: the next barrier is at the loop top
+        // With a mask, its values are read first, and a sub-tile whose mask is -inf for every
+        // (query, key) of the wave is skipped like an invisible one (key padding): its
+        // probabilities are exactly 0.  Queries past L count as fully masked.
+        float mv[MASK ? NT : 1][16];
+        if constexpr (MASK) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                bool any_open = false;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
+                    mv[kt][r] = (live[kt] && key < s.S && qi < s.L) ? mrow[key] : -INFINITY;
+                    any_open |= mv[kt][r] != -INFINITY;
+                }
+                live[kt] = live[kt] && __any(any_open);
+            }
+        }
+        bool any_live = false;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) any_live |= live[kt];
+        if (!any_live) return;  // nothing visible: the next barrier is at the loop top
         const bool edge = n0 + BN > s.S || (CAUSAL && n0 + BN - 1 > wave_last_q - 31);
 
         // S^T = K Q^T: rows are keys, columns are this wave's 32 queries.
@@ -259,10 +279,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                if (MASK) {
-                    const int key = n0 + kt * 32 + acc_row(r, g);
-                    const float mv = (key < s.S && qi < s.L) ? mrow[key] : 0.f;
-                    sacc[kt][r] = (sacc[kt][r] * s.scale + mv) * kLog2e;
+                if constexpr (MASK) {
+                    sacc[kt][r] = (sacc[kt][r] * s.scale + mv[kt][r]) * kLog2e;
                 } else {
                     sacc[kt][r] *= s.scale_log2;
                 }
@@ -359,9 +377,11 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     const int nqt = (a.s.L + kBM - 1) / kBM;
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
     const bool mask = a.s.mask != nullptr;
-    if (a.s.vec && !mask) {  // (the masked kernels keep register staging: fewer VGPRs)
+    if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
             return_if(launch(fwd_f32_kernel<D, BN, true, false, true>, grid, block, st, a));
+        else if (mask)
+            return_if(launch(fwd_f32_kernel<D, BN, false, true, true>, grid, block, st, a));
         else
             return_if(launch(fwd_f32_kernel<D, BN, false, false, true>, grid, block, st, a));
     } else if (a.s.causal && mask) {
