@@ -35,7 +35,7 @@ DEVI uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, 
 DEVI uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 template <int D>
-struct BwdSmemBf16 {
+struct alignas(16) BwdSmemBf16 {
     __bf16 qn[kBM][D + 8];
     __bf16 don[kBM][D + 8];
     __bf16 qt[D][kBM + 4];

@@ -31,7 +31,7 @@ constexpr int kBN = 32 * kWaves;  // keys per workgroup
 constexpr int kBM = 32;           // queries per step
 
 template <int D>
-struct BwdSmem {
+struct alignas(16) BwdSmem {
     // K rows, read by the dQ product with lanes along d and four keys per step: a row stride
     // of D + 16 words puts the four key rows of one read in different 16-bank windows.
     float k[kBN][D + 16];

@@ -31,7 +31,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
-struct FwdSmemBf16 {
+struct alignas(16) FwdSmemBf16 {
     __bf16 k[kBN][D + 8];   // row stride = D/2 + 4 words: ds_read_b128 conflict-free
     // [d][key] with the two middle 4-key groups of every 16 swapped (see vt_col), so a lane's
     // 8 keys of one MFMA step are contiguous; row stride 36 words: ds_read_b128 conflict-free.

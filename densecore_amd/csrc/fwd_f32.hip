@@ -30,7 +30,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;
 
 template <int D, int BN>
-struct FwdSmem {
+struct alignas(16) FwdSmem {
     float k[BN][D + 4];
     float v[BN][D + 4];
 };
