@@ -66,6 +66,21 @@ template <typename T> DEVI T from_f32(float x);
 template <> DEVI float from_f32<float>(float x) { return x; }
 template <> DEVI __bf16 from_f32<__bf16>(float x) { return static_cast<__bf16>(x); }
 
+// One global_load_lds_dwordx4: lane i's 16 bytes at `src` land at LDS `dst` + 16 i (`dst` is
+// wave-uniform; lanes switched off by EXEC write nothing).  Written as inline assembly so that
+// the compiler's wait-count pass does not treat the transfer as aliasing every later LDS read,
+// which would make each tile wait for the next tile's loads; the caller waits (vmcnt(0) +
+// barrier) before reading a filled buffer.
+DEVI void lds_dma16(const void *src, void *dst) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
+DEVI void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // Launches `kernel` and returns the status of this launch alone (hipGetLastError would also
 // report errors left behind by unrelated earlier calls in the process).
 template <typename... Params, typename... Args>

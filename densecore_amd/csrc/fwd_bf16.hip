@@ -7,15 +7,24 @@
 // the only bf16 rounding left is the output's own.  Output is bf16, lse float32.
 //
 //   * 4 waves x 32 queries per workgroup; queries stay in VGPRs as bf16x8 B operands of
-//     S^T = K Q^T (keys x queries), so the softmax state is per lane as in the fp32 kernel;
-//   * K tiles are staged naturally in LDS ([key][d], ds_read_b128 along d);
-//   * V tiles are transposed on their way into LDS ([d][key]): each thread loads a 4-key x
-//     8-dim block (four 16-byte rows), transposes it in registers with byte permutes and
-//     writes eight 8-byte columns, so that O^T += V^T P^T reads 4 consecutive keys per lane;
-//   * P goes from the S^T accumulator straight into the bf16 B operand (the reduction index of
-//     the MFMA is permuted to match the accumulator's row order);
+//     S^T = K Q^T (keys x queries), so the softmax state is per lane;
+//   * K and V tiles of 64 keys are double-buffered in LDS in their natural [key][d] layout and
+//     filled by global_load_lds_dwordx4 while the previous tile is computed (no VGPR staging);
+//   * O^T += V^T P^T takes V^T straight from the [key][d] tile with ds_read_b64_tr_b16 (each
+//     16-lane group reads a 4-key x 16-dim block and gets it transposed: lane j of the group
+//     receives element j % 4 of the 8 bytes read by lanes j / 4, 4 + j / 4, 8 + j / 4 and
+//     12 + j / 4), and P straight from the S^T accumulator (the MFMA reduction index is
+//     permuted to the accumulator's row order: registers 8u..8u+7 of a lane in half g hold
+//     keys 16u + {4g..4g+3, 8+4g..8+4g+3});
+//   * LDS rows are padded instead of swizzled, so every address in the inner loop is a base
+//     plus a constant: K rows are D/8 + 1 16-byte chunks apart (an odd count: ds_read_b128 of
+//     16 consecutive rows hits 16 different bank groups) and V rows D/8 + 4 chunks apart (the
+//     eight rows of one transposed read fall into four different 64-byte bank groups);
 //   * the running max moves only when a tile's max exceeds it by more than 8 (base 2), so the
-//     output accumulator is rarely rescaled.
+//     output accumulator is rarely rescaled;
+//   * workgroups are ordered (batch*head)-major, longest causal tile first, and spread so that
+//     the blocks of one (batch, head) run on the same XCD (blocks are dealt to the 8 XCDs
+//     round-robin), which keeps its K/V in that XCD's L2.
 #include "common.hpp"
 #include "params.hpp"
 
@@ -24,234 +33,249 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 32 * kWaves;
-constexpr int kBN = 64;
+constexpr int kBM = 32 * kWaves;  // queries per workgroup
+constexpr int kBN = 64;           // keys per tile
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
-struct alignas(16) FwdSmemBf16 {
-    __bf16 k[kBN][D + 8];   // row stride = D/2 + 4 words: ds_read_b128 conflict-free
-    // [d][key] with the two middle 4-key groups of every 16 swapped (see vt_col), so a lane's
-    // 8 keys of one MFMA step are contiguous; row stride 36 words: ds_read_b128 conflict-free.
-    __bf16 vt[D][kBN + 8];
+struct TileGeom {
+    static constexpr int C = D / 8;                    // 16-byte chunks per row
+    static constexpr int KS = C + 1;                   // K row stride, chunks
+    static constexpr int VS = C % 8 == 0 ? C + 4 : C;  // V row stride, chunks
+    static constexpr int KSLOTS = kBN * KS, VSLOTS = kBN * VS;
+    static constexpr int KI = (KSLOTS + 63) / 64, VI = (VSLOTS + 63) / 64;  // wave-wide transfers
+    static constexpr int KIW = (KI + kWaves - 1) / kWaves, VIW = (VI + kWaves - 1) / kWaves;
 };
 
-// Column of 4-key group kb4 in vt: inside each 16 keys the groups are stored 0, 2, 1, 3, so that
-// the keys {4g..4g+3, 8+4g..8+4g+3} a half-wave g feeds one bf16 MFMA step sit at 8g..8g+7.
-DEVI int vt_col(int kb4) {
-    const int grp = kb4 & 3;
-    return (kb4 & ~3) * 4 + (grp == 1 ? 2 : grp == 2 ? 1 : grp) * 4;
-}
-
-// Low / high 16 bits of two dwords packed into one: (a.lo, b.lo) and (a.hi, b.hi).
-DEVI uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-DEVI uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
-// One thread's share of a K/V tile: K chunks of 8 dims, and one 4-key x 8-dim V block.
+// One K/V tile: padded rows of bf16 as 16-byte chunks.
 template <int D>
-struct StageBf16 {
-    static constexpr int KCH = kBN * D / 8;          // 16-byte K chunks per tile
-    static constexpr int KN = (KCH + kThreads - 1) / kThreads;
-    static constexpr int VBLK = (kBN / 4) * (D / 8); // 4x8 V blocks per tile
-    static constexpr int VN = (VBLK + kThreads - 1) / kThreads;
-    u32x4 k[KN];
-    u32x4 v[VN][4];
+struct alignas(16) KVTileBf16 {
+    u32x4 k[TileGeom<D>::KI * 64];
+    u32x4 v[TileGeom<D>::VI * 64];
+};
 
-    // vec: E == D and 16-byte aligned rows.  Otherwise element loads with bounds.
-    DEVI void load(const __bf16 *kb, const __bf16 *vb, int n0, int S, int E, bool vec, int tid) {
-#pragma unroll
-        for (int j = 0; j < KN; ++j) {
-            const int i = tid + kThreads * j;
-            const int r = i / (D / 8), c = (i % (D / 8)) * 8, key = n0 + r;
-            k[j] = load8(kb, key, c, S, E, vec && i < KCH, i < KCH);
-        }
-#pragma unroll
-        for (int j = 0; j < VN; ++j) {
-            const int blk = tid + kThreads * j;
-            const int kb4 = blk / (D / 8), c = (blk % (D / 8)) * 8;
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                v[j][u] = load8(vb, n0 + kb4 * 4 + u, c, S, E, vec && blk < VBLK, blk < VBLK);
-        }
-    }
-    static DEVI u32x4 load8(const __bf16 *base, int key, int c, int S, int E, bool vec, bool valid) {
-        if (vec && key < S) return *reinterpret_cast<const u32x4 *>(base + (int64_t)key * D + c);
-        u32x4 x = {0u, 0u, 0u, 0u};
-        if (valid && key < S) {
+// Fill `t` with keys [n0, n0 + kBN): slot s of a matrix holds chunk s % stride of row
+// s / stride; pad slots are skipped, rows past S are zero.
+template <int D, bool VEC>
+DEVI void fill_tile(KVTileBf16<D> &t, const __bf16 *kb, const __bf16 *vb, int n0, int S, int E,
+                    int wave, int lane) {
+    using G = TileGeom<D>;
+    auto one = [&](u32x4 *dst, const __bf16 *src, int stride, int nslots, int j) {
+        const int inst = wave + kWaves * j;
+        const int slot = inst * 64 + lane;
+        const int row = slot / stride, chunk = slot % stride, key = n0 + row;
+        if (slot >= nslots || chunk >= G::C) return;
+        if (VEC && key < S) {
+            lds_dma16(src + (int64_t)key * D + chunk * 8, dst + inst * 64);
+        } else if (VEC) {
+            dst[slot] = u32x4{0u, 0u, 0u, 0u};
+        } else {
             uint16_t h[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                h[e] = c + e < E ? __builtin_bit_cast(uint16_t, base[(int64_t)key * E + c + e])
-                                 : (uint16_t)0;
+            for (int e = 0; e < 8; ++e) {
+                const int d = chunk * 8 + e;
+                h[e] = (key < S && d < E) ? __builtin_bit_cast(uint16_t, src[(int64_t)key * E + d])
+                                          : (uint16_t)0;
+            }
+            u32x4 x;
 #pragma unroll
             for (int w = 0; w < 4; ++w) x[w] = (uint32_t)h[2 * w] | ((uint32_t)h[2 * w + 1] << 16);
+            dst[slot] = x;
         }
-        return x;
-    }
-    DEVI void store(FwdSmemBf16<D> &sm, int tid) const {
+    };
 #pragma unroll
-        for (int j = 0; j < KN; ++j) {
-            const int i = tid + kThreads * j;
-            if (i < KCH) {
-                const int r = i / (D / 8), c = (i % (D / 8)) * 8;
-                *reinterpret_cast<u32x4 *>(&sm.k[r][c]) = k[j];
-            }
-        }
+    for (int j = 0; j < G::KIW; ++j) one(t.k, kb, G::KS, G::KSLOTS, j);
 #pragma unroll
-        for (int j = 0; j < VN; ++j) {
-            const int blk = tid + kThreads * j;
-            if (blk >= VBLK) continue;
-            const int kb4 = blk / (D / 8), c = (blk % (D / 8)) * 8;
-            // Column e of the 4x8 block = (row0[e], row1[e], row2[e], row3[e]).
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const u32x2 even = {pack_lo(v[j][0][w], v[j][1][w]), pack_lo(v[j][2][w], v[j][3][w])};
-                const u32x2 odd = {pack_hi(v[j][0][w], v[j][1][w]), pack_hi(v[j][2][w], v[j][3][w])};
-                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w][vt_col(kb4)]) = even;
-                *reinterpret_cast<u32x2 *>(&sm.vt[c + 2 * w + 1][vt_col(kb4)]) = odd;
-            }
-        }
-    }
-};
+    for (int j = 0; j < G::VIW; ++j) one(t.v, vb, G::VS, G::VSLOTS, j);
+}
 
-template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
-    constexpr int NT = kBN / 32;
-    constexpr int KS = D / 16;  // MFMA k-steps over the head dim
-    __shared__ FwdSmemBf16<D> sm;
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(FwdArgs a) {
+    using G = TileGeom<D>;
+    constexpr int NT = kBN / 32;  // 32-key sub-tiles per tile
+    constexpr int KSTEP = D / 16; // MFMA k-steps over the head dim
+    constexpr int NDT = D / 32;   // 32-dim output tiles
+    __shared__ KVTileBf16<D> sm[2];
 
     const AttnShape &s = a.s;
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches stay scalar
     const int BH = s.B * s.H;
     const int nqt = (s.L + kBM - 1) / kBM;
-    const int bid = blockIdx.x;
-    const int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;
-    const int bh = bid % BH, b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
+    const int nblk = gridDim.x;
+    int w = blockIdx.x;
+    if ((nblk & 7) == 0) w = (w & 7) * (nblk >> 3) + (w >> 3);
+    const int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
     const int q0 = qt * kBM;
-    const int qi = q0 + wave * 32 + lr;
-    const int wave_last_q = q0 + wave * 32 + 31;
+    const int qi = q0 + wave * 32 + lr;  // this lane's query
+    const int wave_q0 = q0 + wave * 32, wave_last_q = wave_q0 + 31;
 
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
 
+    // Scores are formed as fma(q.k, c, -m) in base-2 units; a negative scale is folded into
+    // the queries (a sign flip, exact) so that the max of the raw products is the max score.
+    const bool neg = s.scale_log2 < 0.f;
+    const float c = MASK ? 1.f : (neg ? -s.scale_log2 : s.scale_log2);
+
     // Queries: step t, half g supplies Q[qi][16t + 8g + 0..7].
-    bf16x8 qreg[KS];
+    bf16x8 qreg[KSTEP];
     {
         const __bf16 *qrow = static_cast<const __bf16 *>(a.q) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
-        for (int t = 0; t < KS; ++t) {
+        for (int t = 0; t < KSTEP; ++t) {
             const int d0 = 16 * t + 8 * g;
-            if (s.vec && qi < s.L) {
+            if (VEC && qi < s.L) {
                 qreg[t] = *reinterpret_cast<const bf16x8 *>(qrow + d0);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     qreg[t][e] = (qi < s.L && d0 + e < s.E) ? qrow[d0 + e] : static_cast<__bf16>(0.f);
             }
+            if (!MASK && neg) {
+                u32x4 x = __builtin_bit_cast(u32x4, qreg[t]);
+                x ^= 0x80008000u;
+                qreg[t] = __builtin_bit_cast(bf16x8, x);
+            }
         }
     }
     const float *mrow = nullptr;
     if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
 
-    f32x16 oacc[D / 32];
+    f32x16 oacc[NDT];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_run = -INFINITY, l_part = 0.f;  // l_part: this half-wave's keys only
 
     const int kv_end = CAUSAL ? min(q0 + kBM, s.S) : s.S;
     const int ntiles = (kv_end + kBN - 1) / kBN;
+    if (ntiles > 0) fill_tile<D, VEC>(sm[0], kb, vb, 0, s.S, s.E, wave, lane);
 
-    StageBf16<D> stage;
-    if (ntiles > 0) stage.load(kb, vb, 0, s.S, s.E, s.vec, tid);
+    // Byte offsets of this lane's fragments inside a tile: K for S^T (row lr, dims 8g..),
+    // V for the transposed read (row 4g + (i >> 2), dims 16 * half + 4 (i & 3)).
+    const int i16 = lane & 15, half = (lane >> 4) & 1;
+    const uint32_t koff = (uint32_t)(lr * G::KS * 16 + g * 16);
+    const uint32_t voff = (uint32_t)((4 * g + (i16 >> 2)) * G::VS * 16 + (16 * half + 4 * (i16 & 3)) * 2);
 
-    for (int t = 0; t < ntiles; ++t) {
+    auto tile = [&](int t) {
         const int n0 = t * kBN;
-        __syncthreads();
-        stage.store(sm, tid);
-        __syncthreads();
-        if (t + 1 < ntiles) stage.load(kb, vb, n0 + kBN, s.S, s.E, s.vec, tid);
+        KVTileBf16<D> &cur = sm[t & 1];
+        if (VEC) wait_vmem();  // this wave's transfers of tile t landed
+        __syncthreads();       // everyone's landed; everyone is done with tile t - 1
+        if (t + 1 < ntiles) fill_tile<D, VEC>(sm[(t + 1) & 1], kb, vb, n0 + kBN, s.S, s.E, wave, lane);
+
+        const char *kbase = reinterpret_cast<const char *>(cur.k) + koff;
+        const char *vbase = reinterpret_cast<const char *>(cur.v) + voff;
+        auto kfrag = [&](int kt, int st) {
+            return *reinterpret_cast<const bf16x8 *>(kbase + kt * 32 * G::KS * 16 + st * 32);
+        };
+        auto vfrag = [&](int kt, int u, int dt) {
+            const char *p = vbase + (kt * 32 + 16 * u) * G::VS * 16 + dt * 64;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(p));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(p + 8 * G::VS * 16));
+            const s16x4 cat[2] = {lo, hi};
+            return __builtin_bit_cast(bf16x8, cat);
+        };
 
         bool live[NT];
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
             live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
+        // With a mask its values are read first; a sub-tile whose mask is -inf for every
+        // (query, key) of the wave is skipped (its probabilities are exactly 0).
+        float mv[MASK ? NT : 1][16];
+        if constexpr (MASK) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                bool any_open = false;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
+                    mv[kt][r] = (live[kt] && key < s.S && qi < s.L) ? mrow[key] : -INFINITY;
+                    any_open |= mv[kt][r] != -INFINITY;
+                }
+                live[kt] = live[kt] && __any(any_open);
+            }
+        }
+        bool any_live = false;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) any_live |= live[kt];
+        if (!any_live) return;
+        const bool edge = n0 + kBN > s.S || (CAUSAL && n0 + kBN - 1 > wave_q0);
 
         f32x16 sacc[NT];
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-        // All sub-tiles live (every tile but the causal diagonal): the sub-tiles' independent
-        // MFMA chains are interleaved.  Otherwise one uniform test per sub-tile, outside its
-        // chain (a test inside the chain makes the compiler copy the accumulator around).
-        auto s_step = [&](int kt, int st) {
-            const bf16x8 kk = *reinterpret_cast<const bf16x8 *>(&sm.k[kt * 32 + lr][16 * st + 8 * g]);
-            sacc[kt] = mfma_bf16(kk, qreg[st], sacc[kt]);
-        };
         if (live[NT - 1]) {
+            // Every sub-tile live: their independent MFMA chains are interleaved.
 #pragma unroll
-            for (int st = 0; st < KS; ++st)
+            for (int st = 0; st < KSTEP; ++st)
 #pragma unroll
-                for (int kt = 0; kt < NT; ++kt) s_step(kt, st);
+                for (int kt = 0; kt < NT; ++kt) sacc[kt] = mfma_bf16(kfrag(kt, st), qreg[st], sacc[kt]);
         } else {
+            // One uniform test per sub-tile, outside its chain.
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) {
                 if (!live[kt]) continue;
 #pragma unroll
-                for (int st = 0; st < KS; ++st) s_step(kt, st);
+                for (int st = 0; st < KSTEP; ++st) sacc[kt] = mfma_bf16(kfrag(kt, st), qreg[st], sacc[kt]);
             }
         }
 
+        if constexpr (MASK) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kt][r] = (sacc[kt][r] * s.scale + mv[kt][r]) * kLog2e;
+        }
+        if (edge) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
+                    if (key >= s.S || (CAUSAL && key > qi) || !live[kt]) sacc[kt][r] = -INFINITY;
+                }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = n0 + kt * 32 + acc_row(r, g);
-                float x;
-                if (MASK) {
-                    const float mv = (key < s.S && qi < s.L) ? mrow[key] : 0.f;
-                    x = (sacc[kt][r] * s.scale + mv) * kLog2e;
-                } else {
-                    x = sacc[kt][r] * s.scale_log2;
-                }
-                if (key >= s.S || (CAUSAL && key > qi) || !live[kt]) x = -INFINITY;
-                sacc[kt][r] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = xor32_max(mx);
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+        mx = xor32_max(mx) * c;
         // Lazy rescaling: the exponent reference m_run moves (and O, l are rescaled) only when
         // some lane's tile max exceeds it by more than 8, so P <= 2^8 and most tiles skip the
         // rescale of the accumulator; out = O / l and lse = m_run + log2(l) are unchanged.
         if (__any(mx > m_run + 8.f)) {
             const float m_new = fmaxf(m_run, mx);
             const float alpha = exp2_fast(m_run - (m_new == -INFINITY ? 0.f : m_new));
-            l_run *= alpha;
+            l_part *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
             m_run = m_new;
         }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float ls = 0.f;
+        const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = exp2_fast(sacc[kt][r] - m_use);
+                const float p = exp2_fast(fmaf(sacc[kt][r], c, neg_m));
                 sacc[kt][r] = p;
-                ls += p;
+                l_part += p;
             }
-        l_run += xor32_add(ls);
 
-        // O^T += V^T P^T, 16 keys per MFMA: registers 8u..8u+7 of the S^T accumulator hold
-        // keys 16u + {4g..4g+3, 8+4g..8+4g+3} of the 32-key sub-tile, stored contiguously in vt.
+        // O^T += V^T P^T, 16 keys per MFMA, P as hi + lo.
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt) {
             if (!live[kt]) continue;
@@ -259,27 +283,29 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
             for (int u = 0; u < 2; ++u) {
                 bf16x8 ph, pl;
                 split_bf16(sacc[kt], 8 * u, ph, pl);
-                const int kc = kt * 32 + 16 * u + 8 * g;
+                bf16x8 va[NDT];
 #pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) {
-                    const bf16x8 va = *reinterpret_cast<const bf16x8 *>(&sm.vt[dt * 32 + lr][kc]);
-                    oacc[dt] = mfma_bf16(va, ph, oacc[dt]);
-                    oacc[dt] = mfma_bf16(va, pl, oacc[dt]);
-                }
+                for (int dt = 0; dt < NDT; ++dt) va[dt] = vfrag(kt, u, dt);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], ph, oacc[dt]);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], pl, oacc[dt]);
             }
         }
-    }
+    };
+    for (int t = 0; t < ntiles; ++t) tile(t);
 
+    const float l_run = xor32_add(l_part);
     if (qi < s.L) {
         const bool empty = l_run == 0.f;
         const float inv = empty ? 0.f : 1.f / l_run;
         __bf16 *orow = static_cast<__bf16 *>(a.out) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; r += 4) {
                 const int d = dt * 32 + acc_row(r, g);
-                if (s.vec) {
+                if (VEC) {
                     const bf16x4 o = {static_cast<__bf16>(oacc[dt][r] * inv),
                                       static_cast<__bf16>(oacc[dt][r + 1] * inv),
                                       static_cast<__bf16>(oacc[dt][r + 2] * inv),
@@ -296,22 +322,25 @@ __global__ __launch_bounds__(kThreads) void fwd_bf16_kernel(FwdArgs a) {
     }
 }
 
-template <int D>
-hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
-    FwdArgs a = args;
-    a.s.vec = args.s.vec && args.s.E == D;
+template <int D, bool VEC>
+hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
     const int nqt = (a.s.L + kBM - 1) / kBM;
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
     const bool mask = a.s.mask != nullptr;
     if (a.s.causal && mask)
-        return_if(launch(fwd_bf16_kernel<D, true, true>, grid, block, st, a));
-    else if (a.s.causal)
-        return_if(launch(fwd_bf16_kernel<D, true, false>, grid, block, st, a));
-    else if (mask)
-        return_if(launch(fwd_bf16_kernel<D, false, true>, grid, block, st, a));
-    else
-        return_if(launch(fwd_bf16_kernel<D, false, false>, grid, block, st, a));
-    return hipSuccess;
+        return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
+    if (a.s.causal)
+        return launch(fwd_bf16_kernel<D, true, false, VEC>, grid, block, st, a);
+    if (mask)
+        return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
+    return launch(fwd_bf16_kernel<D, false, false, VEC>, grid, block, st, a);
+}
+
+template <int D>
+hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
+    FwdArgs a = args;
+    a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked 16-byte alignment; E must fill D
+    return a.s.vec ? launch_dv<D, true>(a, st) : launch_dv<D, false>(a, st);
 }
 
 }  // namespace

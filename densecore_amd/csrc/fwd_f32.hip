@@ -97,17 +97,6 @@ DEVI int swz(int row) {
     return (row ^ ((row & 4) << 1)) & (D / 4 - 1);
 }
 
-// One global_load_lds_dwordx4: lane i's 16 bytes at `src` land at LDS `dst` + 16 i (`dst` is
-// wave-uniform).  Written as inline assembly so that the compiler's wait-count pass does not
-// treat the transfer as aliasing every later LDS read, which would make each tile wait for the
-// next tile's loads; the caller waits (vmcnt(0) + barrier) before reading a filled buffer.
-DEVI void lds_dma16(const float *src, float *dst) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src)
-                 : "memory", "m0");
-}
-
 // Issue this wave's share of tile [n0, n0 + BN) into buffer `buf` (keys past the end read a
 // valid row, S - 1; their scores are -inf, so they contribute nothing).
 template <int D, int BN>
