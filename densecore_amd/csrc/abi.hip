@@ -85,9 +85,8 @@ dc_status launched(hipError_t e) {
 }
 
 size_t bwd_ws(const dc::AttnShape &s, bool bf16) {
-    size_t n = round_up((size_t)s.B * s.H * s.L * sizeof(float));  // dsum
-    if (bf16) n += round_up((size_t)s.B * s.H * s.L * s.E * sizeof(float));  // dq accumulator
-    return n;
+    (void)bf16;  // both dtypes: dsum only (float32 accumulates dQ in its output)
+    return round_up((size_t)s.B * s.H * s.L * sizeof(float));
 }
 
 size_t decode_ws(const dc::AttnShape &s) {
@@ -162,8 +161,7 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     a.dout = grad_out, a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
     a.dq = dq, a.dk = dk, a.dv = dv;
     a.dsum = reinterpret_cast<float *>(ws);
-    a.dq_acc = bf16 ? reinterpret_cast<float *>(ws + round_up((size_t)s.B * s.H * s.L * 4))
-                    : static_cast<float *>(dq);
+    a.dq_acc = bf16 ? nullptr : static_cast<float *>(dq);
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
     return launched(dc::launch_bwd_bf16(a, strm));

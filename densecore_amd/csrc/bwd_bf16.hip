@@ -1,21 +1,33 @@
 // bfloat16 attention backward (fp32 accumulation) on CDNA4 MFMA (v_mfma_f32_32x32x16_bf16).
 //
 // Same mathematics as the float32 backward and DenseCore's torch_attention::backward
-// (src/torch_attention.rs:286-468) on bf16 inputs; everything accumulates in float32 and P
-// and dS enter their products as two bf16 terms each (hi = bf16(x), lo = bf16(x - hi)), so
-// they are carried to about 2^-17.  dK and dV are written as bf16; dQ is accumulated in a
-// float32 workspace with atomics and converted at the end.
+// (src/torch_attention.rs:286-468) on bf16 inputs:
+//   dsum = rowsum(dO * O);  P = exp(scale * q k^T + mask - lse) (0 where causal-masked);
+//   dV = P^T dO;  dP = dO V^T;  dS = P * (dP - dsum);  dQ = scale dS K;  dK = scale dS^T Q,
+// accumulating over the query heads that share a kv head (:321-324).  Everything accumulates
+// in float32; P and dS enter their products as two bf16 terms each (hi = bf16(x),
+// lo = bf16(x - hi)), so they are carried to about 2^-17, and the only bf16 roundings left
+// are those of the outputs.
 //
-// Blocking (per workgroup: 128 keys of one (batch, kv head), 4 waves x 32 keys):
-//   * K and V rows of the wave's keys stay in VGPRs as bf16x8 B operands;
-//   * each step stages 32 queries of Q and dO in LDS twice: as rows ([query][d], A operands of
-//     S = Q K^T and dP = dO V^T) and transposed ([d][query], A operands of dV^T = dO^T P and
-//     dK^T = Q^T dS).  The transpose is done in registers on 4x8 blocks, as in the forward;
-//   * the next step's Q and dO blocks are loaded into registers while a step computes;
-//   * dQ = dS K: the four waves write dS (hi and lo) into one shared 32 x 128 LDS tile, and after
-//     the next barrier each wave multiplies its share of it by the workgroup's K tile (kept
-//     transposed in LDS, [d][key]) into disjoint 16 x 16 blocks of dQ, one global atomic per
-//     element per workgroup step.
+// Two kernels, neither with atomics (dQ is deterministic):
+//   * bwd_dkdv_bf16_kernel (keys stationary): a workgroup of 8 waves owns 128 keys of one
+//     (batch, kv head); waves w and w + 4 own the same 32 keys and split each 64-query step.
+//     K and V tiles stay in LDS; per step, Q and dO tiles stream in by global_load_lds while
+//     the previous step computes.  S = Q K^T and dP = dO V^T have queries as rows, so P and
+//     dS feed dV^T += dO^T P and dK^T += Q^T dS straight from the accumulators, with dO^T and
+//     Q^T read from the [query][d] tiles by ds_read_b64_tr_b16.  The two waves' partial dK,
+//     dV are summed through LDS at the end.
+//   * bwd_dq_bf16_kernel (queries stationary, the forward's structure): a workgroup of 4
+//     waves owns 128 queries, keeps Q and dO in VGPRs and streams 64-key K/V tiles;
+//     S^T = K Q^T and dP^T = V dO^T have keys as rows, so dS^T feeds dQ^T += K^T dS^T
+//     from the accumulator, with K^T read from the [key][d] tile by ds_read_b64_tr_b16.
+//     S and dP are computed twice overall (here and in the dK/dV kernel).
+// A pre-kernel forms dsum.
+//
+// LDS tiles are chunk-major: 16-byte chunk c of row r sits at slot c * (R + 4) + r (R rows).
+// A row read (lanes = 32 consecutive rows, one chunk) is 512 contiguous bytes, and a
+// transposed read (8 rows x 4 chunks x 8 bytes) hits every bank exactly twice; all inner-loop
+// addresses are a per-lane base plus a constant.
 #include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
@@ -23,181 +35,177 @@
 namespace dc {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBN = 32 * kWaves;
-constexpr int kBM = 32;
-
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-DEVI uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-DEVI uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
-template <int D>
-struct alignas(16) BwdSmemBf16 {
-    __bf16 qn[kBM][D + 8];
-    __bf16 don[kBM][D + 8];
-    __bf16 qt[D][kBM + 4];
-    __bf16 dot[D][kBM + 4];
-    __bf16 kt[D][kBN + 8];
-    __bf16 ds[2][kBM][kBN + 8];  // dS of the step as hi and lo bf16 parts, all four waves' keys
-    float lse[kBM];
-    float dsum[kBM];
+template <int R, int D>
+struct CMTile {
+    static constexpr int C = D / 8;        // 16-byte chunks per row
+    static constexpr int P = R + 4;        // slots per chunk (4 pad slots)
+    static constexpr int SLOTS = C * P;
+    static constexpr int NI = (SLOTS + 63) / 64;  // wave-wide transfers per tile
+    static constexpr int CS = P * 16;      // chunk stride, bytes
 };
 
-// 16 bytes (8 bf16) of row `row` at column c of a (rows, E) bf16 matrix, zero outside.
-DEVI u32x4 load8(const __bf16 *base, int row, int rows, int c, int E, bool vec, int D) {
-    if (vec && row < rows) return *reinterpret_cast<const u32x4 *>(base + (int64_t)row * D + c);
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (row < rows) {
-        uint16_t h[8];
+// Transfers first, first + step, ... (count of them) of a chunk-major tile holding rows
+// [0, nrows) of `src` (row stride E elements); rows past nrows and dims past E are zero.
+template <int R, int D, bool VEC>
+DEVI void fill_cm(u32x4 *dst, const __bf16 *src, int nrows, int E, int first, int step,
+                  int count, int lane) {
+    using T = CMTile<R, D>;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            h[e] = c + e < E ? __builtin_bit_cast(uint16_t, base[(int64_t)row * E + c + e]) : (uint16_t)0;
+    for (int j = 0; j < count; ++j) {
+        const int inst = first + step * j;
+        if (inst >= T::NI) break;  // wave-uniform
+        const int slot = inst * 64 + lane;
+        const int chunk = slot / T::P, row = slot % T::P;
+        if (slot >= T::SLOTS || row >= R) continue;
+        if (VEC && row < nrows) {
+            lds_dma16(src + (int64_t)row * D + chunk * 8, dst + inst * 64);
+        } else if (VEC) {
+            dst[slot] = u32x4{0u, 0u, 0u, 0u};
+        } else {
+            uint16_t h[8];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) x[w] = (uint32_t)h[2 * w] | ((uint32_t)h[2 * w + 1] << 16);
+            for (int e = 0; e < 8; ++e) {
+                const int d = chunk * 8 + e;
+                h[e] = (row < nrows && d < E) ? __builtin_bit_cast(uint16_t, src[(int64_t)row * E + d])
+                                              : (uint16_t)0;
+            }
+            u32x4 x;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) x[w] = (uint32_t)h[2 * w] | ((uint32_t)h[2 * w + 1] << 16);
+            dst[slot] = x;
+        }
     }
-    return x;
 }
 
-// Writes a 4-row x 8-column block (rows r0..r0+3, columns c..c+7) both as rows of `nat`
-// and as columns of `tr` (tr[c + e][r0 .. r0 + 3]).
-template <int NS, int TS>
-DEVI void store_block(__bf16 (*nat)[NS], __bf16 (*tr)[TS], const u32x4 (&v)[4], int r0, int c) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4 *>(&nat[r0 + u][c]) = v[u];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const u32x2 even = {pack_lo(v[0][w], v[1][w]), pack_lo(v[2][w], v[3][w])};
-        const u32x2 odd = {pack_hi(v[0][w], v[1][w]), pack_hi(v[2][w], v[3][w])};
-        *reinterpret_cast<u32x2 *>(&tr[c + 2 * w][r0]) = even;
-        *reinterpret_cast<u32x2 *>(&tr[c + 2 * w + 1][r0]) = odd;
-    }
+// Row fragment (MFMA operand with rows on lanes): rows row0 + (l % 32), dims 16 st + 8 (l / 32)
+// + 0..7.  `lanebase` = (l % 32) * 16 + (l / 32) * CS.
+template <int R, int D>
+DEVI bf16x8 row_frag(const u32x4 *tile, uint32_t lanebase, int row0, int st) {
+    using T = CMTile<R, D>;
+    const char *p = reinterpret_cast<const char *>(tile) + lanebase + row0 * 16 + 2 * st * T::CS;
+    return *reinterpret_cast<const bf16x8 *>(p);
 }
 
-// One step's Q and dO as 4x8 blocks in registers (loaded during the previous step).
+// Transposed fragment (MFMA operand with dims on lanes): dim 32 dt + (l % 32), rows
+// row0 + {4g..4g+3, 8+4g..8+4g+3} (g = l / 32), read by two ds_read_b64_tr_b16.
+// `lanebase` = (4g + (i >> 2)) * 16 + 8 (i & 1) + (2 half + ((i & 3) >> 1)) * CS, i = l % 16,
+// half = (l / 16) % 2.
+template <int R, int D>
+DEVI bf16x8 tr_frag(const u32x4 *tile, uint32_t lanebase, int row0, int dt) {
+    using T = CMTile<R, D>;
+    const char *p = reinterpret_cast<const char *>(tile) + lanebase + row0 * 16 + 4 * dt * T::CS;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(p));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4 *)(p + 8 * 16));
+    const s16x4 cat[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, cat);
+}
+
+template <int R, int D>
+DEVI uint32_t row_lanebase(int lane) {
+    return (uint32_t)((lane & 31) * 16 + (lane >> 5) * CMTile<R, D>::CS);
+}
+template <int R, int D>
+DEVI uint32_t tr_lanebase(int lane) {
+    const int i = lane & 15, half = (lane >> 4) & 1, g = lane >> 5;
+    return (uint32_t)((4 * g + (i >> 2)) * 16 + 8 * (i & 1) + (2 * half + ((i & 3) >> 1)) * CMTile<R, D>::CS);
+}
+
+// Logical block index: blocks are dealt to the 8 XCDs round-robin, so consecutive logical
+// indices are spread to land on the same XCD (whose L2 then holds their shared K/V or Q/dO).
+DEVI int logical_block() {
+    const int n = gridDim.x, w = blockIdx.x;
+    return (n & 7) == 0 ? (w & 7) * (n >> 3) + (w >> 3) : w;
+}
+
+// ---------------------------------------------------------------------------------------
+// dK / dV (keys stationary)
+// ---------------------------------------------------------------------------------------
+constexpr int kKW = 8;             // waves
+constexpr int kKThreads = 64 * kKW;
+constexpr int kKN = 128;           // keys per workgroup
+constexpr int kKM = 64;            // queries per step
+
 template <int D>
-struct QStageBf16 {
-    static constexpr int QBLK = (kBM / 4) * (D / 8);  // blocks per tensor
-    static constexpr int N = (2 * QBLK + kThreads - 1) / kThreads;
-    u32x4 v[N][4];
-    float lse, dsum;
-
-    DEVI void load(const __bf16 *qb, const __bf16 *gb, const float *lseb, const float *dsumb,
-                   int m0, int L, int E, bool vec, int tid) {
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-            const int blk = tid + kThreads * j;
-            const bool isq = blk < QBLK;
-            const int bi = isq ? blk : blk - QBLK;
-            const int r0 = (bi / (D / 8)) * 4, c = (bi % (D / 8)) * 8;
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                v[j][u] = blk < 2 * QBLK ? load8(isq ? qb : gb, m0 + r0 + u, L, c, E, vec, D)
-                                         : u32x4{0u, 0u, 0u, 0u};
-        }
-        if (tid < kBM) {
-            const int qq = m0 + tid;
-            lse = qq < L ? lseb[qq] : INFINITY;
-            dsum = qq < L ? dsumb[qq] : 0.f;
-        }
-    }
-    DEVI void store(BwdSmemBf16<D> &sm, int tid) const {
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-            const int blk = tid + kThreads * j;
-            if (blk >= 2 * QBLK) continue;
-            const bool isq = blk < QBLK;
-            const int bi = isq ? blk : blk - QBLK;
-            const int r0 = (bi / (D / 8)) * 4, c = (bi % (D / 8)) * 8;
-            if (isq)
-                store_block(sm.qn, sm.qt, v[j], r0, c);
-            else
-                store_block(sm.don, sm.dot, v[j], r0, c);
-        }
-        if (tid < kBM) sm.lse[tid] = lse, sm.dsum[tid] = dsum;
-    }
+struct alignas(16) DkdvSmem {
+    using TK = CMTile<kKN, D>;
+    using TQ = CMTile<kKM, D>;
+    struct Main {
+        u32x4 k[TK::NI * 64];
+        u32x4 v[TK::NI * 64];
+        u32x4 q[2][TQ::NI * 64];
+        u32x4 o[2][TQ::NI * 64];
+        float lse[2][kKM];
+        float dsum[2][kKM];
+    };
+    // End of the sweep: the second wave of each pair hands its partial dK^T, dV^T over.
+    struct Red {
+        float acc[4][2 * (D / 32)][16][64];
+    };
+    union {
+        Main m;
+        Red r;
+    };
 };
 
-// dQ[m0 .. m0+31][:] += scale * dS K for the step whose dS (hi, lo) is in sm.ds: the 32 x D
-// tile is split into 16 x 16 blocks, D/32 per wave, each reduced over `nkeys` keys with
-// v_mfma_f32_16x16x32_bf16 (lane l supplies A[l%16][8(l/16)..+7], B[8(l/16)..+7][l%16] and
-// holds C[4(l/16) + v][l%16]); one global atomic per element per workgroup step.
-template <int D>
-DEVI void dq_product(const BwdSmemBf16<D> &sm, float *dqb, int m0, int nkeys, int L, int E,
-                     float scale, int wave, int lane) {
-    constexpr int TPW = D / 32;
-    const int r16 = lane & 15, c4 = lane >> 4;
-    const int qh = wave >> 1, dbase = (wave & 1) * (D / 2);
-    f32x4 acc[TPW];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int steps = (nkeys + 31) / 32;
-    for (int st = 0; st < steps; ++st) {
-        const int kc = 32 * st + 8 * c4;
-        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&sm.ds[0][qh * 16 + r16][kc]);
-        const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&sm.ds[1][qh * 16 + r16][kc]);
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-            const bf16x8 kk = *reinterpret_cast<const bf16x8 *>(&sm.kt[dbase + 16 * j + r16][kc]);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, kk, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, kk, acc[j], 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-        const int d = dbase + 16 * j + r16;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int qq = m0 + qh * 16 + 4 * c4 + v;
-            if (qq < L && d < E) unsafeAtomicAdd(dqb + (int64_t)qq * E + d, acc[j][v] * scale);
-        }
-    }
-}
-
-template <int D, bool CAUSAL, bool MASK>
-__global__ __launch_bounds__(kThreads) void bwd_bf16_kernel(BwdArgs a) {
-    constexpr int KS = D / 16;
-    constexpr int NDT = D / 32;
-    __shared__ BwdSmemBf16<D> sm;
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
+    using TK = CMTile<kKN, D>;
+    using TQ = CMTile<kKM, D>;
+    constexpr int KSTEP = D / 16, NDT = D / 32;
+    __shared__ DkdvSmem<D> sm;
 
     const AttnShape &s = a.s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
-    const int BHk = s.B * s.Hkv;
-    const int bid = blockIdx.x;
-    const int ktile = bid / BHk;
-    const int bhk = bid % BHk, b = bhk / s.Hkv, hk = bhk % s.Hkv;
-    const int n0 = ktile * kBN;
-    const int kw0 = n0 + wave * 32;
-    const int key = kw0 + lr;
-    const int D_ = D;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kw = wave & 3, qh = wave >> 2;
+    const int nkt = (s.S + kKN - 1) / kKN;
+    const int w = logical_block();
+    const int bhk = w / nkt, n0 = (w % nkt) * kKN;  // causal: small n0 (most queries) first
+    const int b = bhk / s.Hkv, hk = bhk % s.Hkv;
+    const int kw0 = n0 + 32 * kw;
+    const int key = kw0 + lr;  // this lane's key column
 
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)bhk * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)bhk * s.S * s.E;
+    const int nkeys = min(kKN, s.S - n0);
+    fill_cm<kKN, D, VEC>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, kKW, (TK::NI + kKW - 1) / kKW, lane);
+    fill_cm<kKN, D, VEC>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, kKW, (TK::NI + kKW - 1) / kKW, lane);
 
-    bf16x8 kreg[KS], vreg[KS];
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-        const u32x4 x = load8(kb, key, s.S, 16 * t + 8 * g, s.E, s.vec, D_);
-        const u32x4 y = load8(vb, key, s.S, 16 * t + 8 * g, s.E, s.vec, D_);
-        kreg[t] = __builtin_bit_cast(bf16x8, x);
-        vreg[t] = __builtin_bit_cast(bf16x8, y);
+    const int m_begin = CAUSAL ? n0 : 0;  // n0 is a multiple of kKM
+    const int per_head = s.L > m_begin ? (s.L - m_begin + kKM - 1) / kKM : 0;
+    const int nsteps = per_head * s.repeat;
+    auto step_bh = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
+    auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kKM; };
+    auto fill_step = [&](int i) {
+        const int bh = step_bh(i), m0 = step_m0(i), buf = i & 1;
+        const int rows = min(kKM, s.L - m0);
+        const int64_t off = ((int64_t)bh * s.L + m0) * s.E;
+        constexpr int cnt = (TQ::NI + kKW - 1) / kKW;
+        fill_cm<kKM, D, VEC>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, kKW, cnt, lane);
+        fill_cm<kKM, D, VEC>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, kKW, cnt, lane);
+    };
+    // lse (+inf past L: P = 0 there) and dsum of a step, one value per lane of waves 0 and 1.
+    auto load_row_stat = [&](int i) -> float {
+        const int bh = step_bh(i), qq = step_m0(i) + lane;
+        if (wave == 0) return qq < s.L ? a.lse[(int64_t)bh * s.L + qq] : INFINITY;
+        return qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
+    };
+    auto store_row_stat = [&](int i, float x) {
+        if (wave == 0) sm.m.lse[i & 1][lane] = x;
+        else sm.m.dsum[i & 1][lane] = x;
+    };
+    if (nsteps > 0) {
+        fill_step(0);
+        if (wave < 2) store_row_stat(0, load_row_stat(0));
     }
-    // The workgroup's K tile, transposed: kt[d][key - n0].
-    for (int blk = tid; blk < (kBN / 4) * (D / 8); blk += kThreads) {
-        const int r0 = (blk / (D / 8)) * 4, c = (blk % (D / 8)) * 8;
-        u32x4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = load8(kb, n0 + r0 + u, s.S, c, s.E, s.vec, D_);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const u32x2 even = {pack_lo(v[0][w], v[1][w]), pack_lo(v[2][w], v[3][w])};
-            const u32x2 odd = {pack_hi(v[0][w], v[1][w]), pack_hi(v[2][w], v[3][w])};
-            *reinterpret_cast<u32x2 *>(&sm.kt[c + 2 * w][r0]) = even;
-            *reinterpret_cast<u32x2 *>(&sm.kt[c + 2 * w + 1][r0]) = odd;
-        }
-    }
+
+    const uint32_t rowb = row_lanebase<kKM, D>(lane);
+    const uint32_t rowbk = row_lanebase<kKN, D>(lane);
+    const uint32_t trb = tr_lanebase<kKM, D>(lane);
 
     f32x16 dk[NDT], dv[NDT];
 #pragma unroll
@@ -205,143 +213,317 @@ __global__ __launch_bounds__(kThreads) void bwd_bf16_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[dt][r] = 0.f, dv[dt][r] = 0.f;
 
-    const int m_begin = CAUSAL ? (n0 / kBM) * kBM : 0;
-    const int per_head = s.L > m_begin ? (s.L - m_begin + kBM - 1) / kBM : 0;
-    const int nsteps = per_head * s.repeat;
-    const int key_end = min(kBN, s.S - n0);
-    auto step_head = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
-    auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kBM; };
-    auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
-    auto qptr = [&](int bh) { return static_cast<const __bf16 *>(a.q) + (int64_t)bh * s.L * s.E; };
-    auto gptr = [&](int bh) { return static_cast<const __bf16 *>(a.dout) + (int64_t)bh * s.L * s.E; };
-
-    QStageBf16<D> stage;
-    if (nsteps > 0) {
-        const int bh = step_head(0);
-        stage.load(qptr(bh), gptr(bh), a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L,
-                   step_m0(0), s.L, s.E, s.vec, tid);
-    }
-    int prev_bh = -1, prev_m0 = 0;
     for (int i = 0; i < nsteps; ++i) {
-        const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
-        __syncthreads();  // the previous step's readers of Q/dO and writers of dS are done
-        if (prev_bh >= 0)
-            dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0),
-                          s.L, s.E, s.scale, wave, lane);
-        stage.store(sm, tid);
-        __syncthreads();  // staged, and the previous dQ product has read sm.ds
+        const int bh = step_bh(i), h = bh - b * s.H, m0 = step_m0(i), buf = i & 1;
+        if (VEC) wait_vmem();
+        __syncthreads();  // step i's tiles landed (and K/V at i = 0); step i - 1 is done
+        float stat = 0.f;
         if (i + 1 < nsteps) {
-            const int nbh = step_head(i + 1);
-            stage.load(qptr(nbh), gptr(nbh), a.lse + (int64_t)nbh * s.L, a.dsum + (int64_t)nbh * s.L,
-                       step_m0(i + 1), s.L, s.E, s.vec, tid);
-        }
-        prev_bh = bh, prev_m0 = m0;
-
-        const bool live = kw0 < s.S && (!CAUSAL || m0 + kBM - 1 >= kw0);
-        if (!live) continue;
-        const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
-
-        f32x16 sacc, pacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
-#pragma unroll
-        for (int t = 0; t < KS; ++t) {
-            const bf16x8 qa = *reinterpret_cast<const bf16x8 *>(&sm.qn[lr][16 * t + 8 * g]);
-            const bf16x8 oa = *reinterpret_cast<const bf16x8 *>(&sm.don[lr][16 * t + 8 * g]);
-            sacc = mfma_bf16(qa, kreg[t], sacc);
-            pacc = mfma_bf16(oa, vreg[t], pacc);
+            if (wave < 2) stat = load_row_stat(i + 1);
+            fill_step(i + 1);
         }
 
-        const bool edge = kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > m0);
+        const int mq = m0 + 32 * qh;  // this wave's 32 queries
+        const bool live = kw0 < s.S && mq < s.L && (!CAUSAL || mq + 31 >= kw0);
+        if (live) {
+            const u32x4 *qt = sm.m.q[buf], *ot = sm.m.o[buf];
+            f32x16 sacc, pacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
+#pragma unroll
+            for (int st = 0; st < KSTEP; ++st) {
+                sacc = mfma_bf16(row_frag<kKM, D>(qt, rowb, 32 * qh, st),
+                                 row_frag<kKN, D>(sm.m.k, rowbk, 32 * kw, st), sacc);
+                pacc = mfma_bf16(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
+                                 row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
+            }
+
+            const bool edge = kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > mq);
+            const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int row0 = 32 * qh + 8 * r4 + 4 * g;  // rows of registers 4 r4 .. 4 r4 + 3
+                const f32x4 ls = *reinterpret_cast<const f32x4 *>(&sm.m.lse[buf][row0]);
+                const f32x4 dsm = *reinterpret_cast<const f32x4 *>(&sm.m.dsum[buf][row0]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 4 * r4 + j, qq = m0 + row0 + j;
+                    // scale * q.k (+ mask) - lse in natural-log units, as the reference forms
+                    // it, then one conversion to base 2.
+                    float x = sacc[r] * s.scale;
+                    if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+                    float p = exp2_fast((x - ls[j]) * kLog2e);
+                    if (edge && (key >= s.S || (CAUSAL && key > qq))) p = 0.f;
+                    sacc[r] = p;
+                    pacc[r] = p * (pacc[r] - dsm[j]);
+                }
+            }
+
+            // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA.
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int row0 = 32 * qh + 16 * u;
+                bf16x8 ph, pl;
+                split_bf16(sacc, 8 * u, ph, pl);
+                bf16x8 fa[NDT];
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(ot, trb, row0, dt);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], ph, dv[dt]);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], pl, dv[dt]);
+                split_bf16(pacc, 8 * u, ph, pl);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(qt, trb, row0, dt);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], ph, dk[dt]);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], pl, dk[dt]);
+            }
+        }
+        if (i + 1 < nsteps && wave < 2) store_row_stat(i + 1, stat);
+    }
+
+    // Sum the two partials of each key group (waves kw and kw + 4) and write dK, dV.  The
+    // reduction buffer overlays the tiles: no transfer may still be in flight (with no steps
+    // the K/V transfers were never waited for).
+    if (VEC) wait_vmem();
+    __syncthreads();
+    if (qh == 1) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                sm.r.acc[kw][dt][r][lane] = dk[dt][r];
+                sm.r.acc[kw][NDT + dt][r][lane] = dv[dt][r];
+            }
+    }
+    __syncthreads();
+    if (qh == 1 || key >= s.S) return;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int qrow = acc_row(r, g), qq = m0 + qrow;
-            // scale * q.k (+ mask) - lse in natural-log units, as the reference forms it,
-            // then one conversion to base 2 for v_exp_f32.
-            float x = sacc[r] * s.scale;
-            if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-            float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
-            if (edge && (key >= s.S || (CAUSAL && key > qq))) p = 0.f;
-            sacc[r] = p;
-            pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
-            const __bf16 hv = static_cast<__bf16>(pacc[r]);
-            sm.ds[0][qrow][wave * 32 + lr] = hv;
-            sm.ds[1][qrow][wave * 32 + lr] = static_cast<__bf16>(pacc[r] - static_cast<float>(hv));
+            dk[dt][r] += sm.r.acc[kw][dt][r][lane];
+            dv[dt][r] += sm.r.acc[kw][NDT + dt][r][lane];
         }
+    __bf16 *dkr = static_cast<__bf16 *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
+    __bf16 *dvr = static_cast<__bf16 *>(a.dv) + ((int64_t)bhk * s.S + key) * s.E;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+            const int d = dt * 32 + acc_row(r, g);
+            if (VEC) {
+                const bf16x4 kx = {static_cast<__bf16>(dk[dt][r] * s.scale),
+                                   static_cast<__bf16>(dk[dt][r + 1] * s.scale),
+                                   static_cast<__bf16>(dk[dt][r + 2] * s.scale),
+                                   static_cast<__bf16>(dk[dt][r + 3] * s.scale)};
+                const bf16x4 vx = {static_cast<__bf16>(dv[dt][r]), static_cast<__bf16>(dv[dt][r + 1]),
+                                   static_cast<__bf16>(dv[dt][r + 2]), static_cast<__bf16>(dv[dt][r + 3])};
+                *reinterpret_cast<bf16x4 *>(dkr + d) = kx;
+                *reinterpret_cast<bf16x4 *>(dvr + d) = vx;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (d + u < s.E) {
+                        dkr[d + u] = static_cast<__bf16>(dk[dt][r + u] * s.scale);
+                        dvr[d + u] = static_cast<__bf16>(dv[dt][r + u]);
+                    }
+            }
+        }
+}
 
-        // dV^T += dO^T P and dK^T += Q^T dS: 16 queries per MFMA, registers 8u..8u+7 hold
-        // queries 16u + {4g..4g+3, 8+4g..8+4g+3}.
+// ---------------------------------------------------------------------------------------
+// dQ (queries stationary)
+// ---------------------------------------------------------------------------------------
+constexpr int kQW = 4;
+constexpr int kQThreads = 64 * kQW;
+constexpr int kQM = 32 * kQW;  // queries per workgroup
+constexpr int kQN = 64;        // keys per tile
+
+template <int D>
+struct alignas(16) DqSmem {
+    using T = CMTile<kQN, D>;
+    u32x4 k[2][T::NI * 64];
+    u32x4 v[2][T::NI * 64];
+};
+
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(BwdArgs a) {
+    using T = CMTile<kQN, D>;
+    constexpr int KSTEP = D / 16, NDT = D / 32, NT = kQN / 32;
+    __shared__ DqSmem<D> sm;
+
+    const AttnShape &s = a.s;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nqt = (s.L + kQM - 1) / kQM;
+    const int w = logical_block();
+    const int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
+    const int q0 = qt * kQM;
+    const int qi = q0 + wave * 32 + lr;
+    const int wave_q0 = q0 + wave * 32, wave_last_q = wave_q0 + 31;
+
+    const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+    const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+
+    // Q and dO rows of this lane's query as B operands (step t, half g: dims 16t + 8g + 0..7).
+    bf16x8 qreg[KSTEP], oreg[KSTEP];
+    {
+        const int64_t ro = ((int64_t)bh * s.L + qi) * s.E;
+        const __bf16 *qrow = static_cast<const __bf16 *>(a.q) + ro;
+        const __bf16 *orow = static_cast<const __bf16 *>(a.dout) + ro;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            bf16x8 ph, pl, sh, sl;
-            split_bf16(sacc, 8 * u, ph, pl);
-            split_bf16(pacc, 8 * u, sh, sl);
-            const int qc = 16 * u + 4 * g;
+        for (int t = 0; t < KSTEP; ++t) {
+            const int d0 = 16 * t + 8 * g;
+            if (VEC && qi < s.L) {
+                qreg[t] = *reinterpret_cast<const bf16x8 *>(qrow + d0);
+                oreg[t] = *reinterpret_cast<const bf16x8 *>(orow + d0);
+            } else {
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const bf16x4 olo = *reinterpret_cast<const bf16x4 *>(&sm.dot[dt * 32 + lr][qc]);
-                const bf16x4 ohi = *reinterpret_cast<const bf16x4 *>(&sm.dot[dt * 32 + lr][qc + 8]);
-                const bf16x4 qlo = *reinterpret_cast<const bf16x4 *>(&sm.qt[dt * 32 + lr][qc]);
-                const bf16x4 qhi = *reinterpret_cast<const bf16x4 *>(&sm.qt[dt * 32 + lr][qc + 8]);
-                const bf16x8 oa = {olo[0], olo[1], olo[2], olo[3], ohi[0], ohi[1], ohi[2], ohi[3]};
-                const bf16x8 qa = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-                dv[dt] = mfma_bf16(oa, ph, dv[dt]);
-                dv[dt] = mfma_bf16(oa, pl, dv[dt]);
-                dk[dt] = mfma_bf16(qa, sh, dk[dt]);
-                dk[dt] = mfma_bf16(qa, sl, dk[dt]);
+                for (int e = 0; e < 8; ++e) {
+                    const bool ok = qi < s.L && d0 + e < s.E;
+                    qreg[t][e] = ok ? qrow[d0 + e] : static_cast<__bf16>(0.f);
+                    oreg[t][e] = ok ? orow[d0 + e] : static_cast<__bf16>(0.f);
+                }
             }
         }
     }
-    __syncthreads();
-    if (prev_bh >= 0)
-        dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0), s.L,
-                      s.E, s.scale, wave, lane);
+    const float lse_q = qi < s.L ? a.lse[(int64_t)bh * s.L + qi] : 0.f;
+    const float dsum_q = qi < s.L ? a.dsum[(int64_t)bh * s.L + qi] : 0.f;
+    const float *mrow = nullptr;
+    if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
 
-    if (key < s.S) {
-        __bf16 *dkr = static_cast<__bf16 *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
-        __bf16 *dvr = static_cast<__bf16 *>(a.dv) + ((int64_t)bhk * s.S + key) * s.E;
+    f32x16 dq[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
+
+    const int kv_end = CAUSAL ? min(q0 + kQM, s.S) : s.S;
+    const int ntiles = (kv_end + kQN - 1) / kQN;
+    constexpr int cnt = (T::NI + kQW - 1) / kQW;
+    auto fill = [&](int t) {
+        const int n0 = t * kQN, rows = min(kQN, s.S - n0);
+        fill_cm<kQN, D, VEC>(sm.k[t & 1], kb + (int64_t)n0 * s.E, rows, s.E, wave, kQW, cnt, lane);
+        fill_cm<kQN, D, VEC>(sm.v[t & 1], vb + (int64_t)n0 * s.E, rows, s.E, wave, kQW, cnt, lane);
+    };
+    if (ntiles > 0) fill(0);
+    const uint32_t rowb = row_lanebase<kQN, D>(lane);
+    const uint32_t trb = tr_lanebase<kQN, D>(lane);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = t * kQN;
+        if (VEC) wait_vmem();
+        __syncthreads();
+        if (t + 1 < ntiles) fill(t + 1);
+        const u32x4 *kt_ = sm.k[t & 1], *vt_ = sm.v[t & 1];
+
+        bool live[NT];
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+            live[kt] = (n0 + kt * 32 < s.S) && (!CAUSAL || n0 + kt * 32 <= wave_last_q);
+        float mv[MASK ? NT : 1][16];
+        if constexpr (MASK) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                bool any_open = false;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + kt * 32 + acc_row(r, g);
+                    mv[kt][r] = (live[kt] && key < s.S && qi < s.L) ? mrow[key] : -INFINITY;
+                    any_open |= mv[kt][r] != -INFINITY;
+                }
+                live[kt] = live[kt] && __any(any_open);
+            }
+        }
+        const bool edge = n0 + kQN > s.S || (CAUSAL && n0 + kQN - 1 > wave_q0);
+
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+            if (!live[kt]) continue;
+            f32x16 sacc, pacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
+#pragma unroll
+            for (int st = 0; st < KSTEP; ++st) {
+                sacc = mfma_bf16(row_frag<kQN, D>(kt_, rowb, 32 * kt, st), qreg[st], sacc);
+                pacc = mfma_bf16(row_frag<kQN, D>(vt_, rowb, 32 * kt, st), oreg[st], pacc);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = n0 + kt * 32 + acc_row(r, g);
+                float x = sacc[r] * s.scale;
+                if (MASK) x += mv[kt][r];
+                float p = exp2_fast((x - lse_q) * kLog2e);
+                if (edge && (key >= s.S || (CAUSAL && key > qi))) p = 0.f;
+                sacc[r] = p * (pacc[r] - dsum_q);  // dS^T
+            }
+            // dQ^T += K^T dS^T, 16 keys per MFMA.
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 sh, sl;
+                split_bf16(sacc, 8 * u, sh, sl);
+                bf16x8 fa[NDT];
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kQN, D>(kt_, trb, 32 * kt + 16 * u, dt);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sh, dq[dt]);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sl, dq[dt]);
+            }
+        }
+    }
+
+    if (qi < s.L) {
+        __bf16 *dqr = static_cast<__bf16 *>(a.dq) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; r += 4) {
                 const int d = dt * 32 + acc_row(r, g);
-                if (s.vec) {
-                    const bf16x4 kx = {static_cast<__bf16>(dk[dt][r] * s.scale),
-                                       static_cast<__bf16>(dk[dt][r + 1] * s.scale),
-                                       static_cast<__bf16>(dk[dt][r + 2] * s.scale),
-                                       static_cast<__bf16>(dk[dt][r + 3] * s.scale)};
-                    const bf16x4 vx = {static_cast<__bf16>(dv[dt][r]), static_cast<__bf16>(dv[dt][r + 1]),
-                                       static_cast<__bf16>(dv[dt][r + 2]), static_cast<__bf16>(dv[dt][r + 3])};
-                    *reinterpret_cast<bf16x4 *>(dkr + d) = kx;
-                    *reinterpret_cast<bf16x4 *>(dvr + d) = vx;
+                if (VEC) {
+                    const bf16x4 o = {static_cast<__bf16>(dq[dt][r] * s.scale),
+                                      static_cast<__bf16>(dq[dt][r + 1] * s.scale),
+                                      static_cast<__bf16>(dq[dt][r + 2] * s.scale),
+                                      static_cast<__bf16>(dq[dt][r + 3] * s.scale)};
+                    *reinterpret_cast<bf16x4 *>(dqr + d) = o;
                 } else {
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        if (d + u < s.E) {
-                            dkr[d + u] = static_cast<__bf16>(dk[dt][r + u] * s.scale);
-                            dvr[d + u] = static_cast<__bf16>(dv[dt][r + u]);
-                        }
+                        if (d + u < s.E) dqr[d + u] = static_cast<__bf16>(dq[dt][r + u] * s.scale);
                 }
             }
     }
+}
+
+template <int D, bool VEC>
+hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
+    const bool mask = a.s.mask != nullptr, causal = a.s.causal;
+    const dim3 gk(((a.s.S + kKN - 1) / kKN) * a.s.B * a.s.Hkv), bk(kKThreads);
+    const dim3 gq(((a.s.L + kQM - 1) / kQM) * a.s.B * a.s.H), bq(kQThreads);
+    if (a.s.S > 0) {
+        if (causal && mask) return_if(launch(bwd_dkdv_bf16_kernel<D, true, true, VEC>, gk, bk, st, a));
+        else if (causal) return_if(launch(bwd_dkdv_bf16_kernel<D, true, false, VEC>, gk, bk, st, a));
+        else if (mask) return_if(launch(bwd_dkdv_bf16_kernel<D, false, true, VEC>, gk, bk, st, a));
+        else return_if(launch(bwd_dkdv_bf16_kernel<D, false, false, VEC>, gk, bk, st, a));
+    }
+    if (a.s.L > 0) {
+        if (causal && mask) return_if(launch(bwd_dq_bf16_kernel<D, true, true, VEC>, gq, bq, st, a));
+        else if (causal) return_if(launch(bwd_dq_bf16_kernel<D, true, false, VEC>, gq, bq, st, a));
+        else if (mask) return_if(launch(bwd_dq_bf16_kernel<D, false, true, VEC>, gq, bq, st, a));
+        else return_if(launch(bwd_dq_bf16_kernel<D, false, false, VEC>, gq, bq, st, a));
+    }
+    return hipSuccess;
 }
 
 template <int D>
 hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
     BwdArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;
-    const int nkt = (a.s.S + kBN - 1) / kBN;
-    const dim3 grid(nkt * a.s.B * a.s.Hkv), block(kThreads);
-    const bool mask = a.s.mask != nullptr;
-    if (a.s.causal && mask)
-        return_if(launch(bwd_bf16_kernel<D, true, true>, grid, block, st, a));
-    else if (a.s.causal)
-        return_if(launch(bwd_bf16_kernel<D, true, false>, grid, block, st, a));
-    else if (mask)
-        return_if(launch(bwd_bf16_kernel<D, false, true>, grid, block, st, a));
-    else
-        return_if(launch(bwd_bf16_kernel<D, false, false>, grid, block, st, a));
-    return hipSuccess;
+    return a.s.vec ? launch_dv<D, true>(a, st) : launch_dv<D, false>(a, st);
 }
 
 }  // namespace
@@ -349,24 +531,12 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st) {
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
     if (rows > 0) {
-        return_if(launch(bwd_pre_kernel<__bf16>, dim3((rows + 15) / 16), dim3(256), st, a));
+        return_if(launch(bwd_pre_kernel<__bf16, false>, dim3((rows + 15) / 16), dim3(256), st, a));
     }
-    if (a.s.B * a.s.Hkv > 0 && a.s.S > 0) {
-        hipError_t e;
-        if (a.s.E <= 32)
-            e = launch_d<32>(a, st);
-        else if (a.s.E <= 64)
-            e = launch_d<64>(a, st);
-        else
-            e = launch_d<128>(a, st);
-        if (e != hipSuccess) return e;
-    }
-    const int64_t n = rows * a.s.E;
-    if (n > 0) {
-        return_if(launch(bwd_dq_convert_kernel<__bf16>, dim3((n + 255) / 256), dim3(256), st, a, n));
-        return hipSuccess;
-    }
-    return hipSuccess;
+    if (a.s.B * a.s.Hkv == 0) return hipSuccess;
+    if (a.s.E <= 32) return launch_d<32>(a, st);
+    if (a.s.E <= 64) return launch_d<64>(a, st);
+    return launch_d<128>(a, st);
 }
 
 }  // namespace dc

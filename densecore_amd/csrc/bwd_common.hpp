@@ -6,8 +6,9 @@
 
 namespace dc {
 
-// dsum[row] = sum_d dO[row][d] * O[row][d]; also clears the float32 dQ accumulator row.
-template <typename T>
+// dsum[row] = sum_d dO[row][d] * O[row][d]; with CLEAR also zeroes the float32 dQ accumulator
+// row (the float32 backward accumulates dQ into its output with atomics).
+template <typename T, bool CLEAR>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
     const AttnShape &s = a.s;
     const int64_t rows = (int64_t)s.B * s.H * s.L;
@@ -21,15 +22,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
     if (part == 0) a.dsum[row] = acc;
-    float *dq = a.dq_acc + row * s.E;
-    for (int d = part; d < s.E; d += 16) dq[d] = 0.f;
-}
-
-// dq[i] = T(dq_acc[i]): the bfloat16 path accumulates dQ in a float32 workspace.
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_dq_convert_kernel(BwdArgs a, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) static_cast<T *>(a.dq)[i] = from_f32<T>(a.dq_acc[i]);
+    if (CLEAR) {
+        float *dq = a.dq_acc + row * s.E;
+        for (int d = part; d < s.E; d += 16) dq[d] = 0.f;
+    }
 }
 
 }  // namespace dc

@@ -332,7 +332,7 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st) {
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
     if (rows > 0) {
-        return_if(launch(bwd_pre_kernel<float>, dim3((rows + 15) / 16), dim3(256), st, a));
+        return_if(launch(bwd_pre_kernel<float, true>, dim3((rows + 15) / 16), dim3(256), st, a));
     }
     if (a.s.B * a.s.Hkv == 0 || a.s.S == 0) return hipSuccess;
     if (a.s.E <= 32) return launch_d<32>(a, st);
