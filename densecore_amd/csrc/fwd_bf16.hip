@@ -102,7 +102,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const AttnShape &s = a.s;
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches stay scalar
-    const int BH = s.B * s.H;
     const int nqt = (s.L + kBM - 1) / kBM;
     const int nblk = gridDim.x;
     int w = blockIdx.x;
