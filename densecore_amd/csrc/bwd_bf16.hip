@@ -28,6 +28,8 @@
 // A row read (lanes = 32 consecutive rows, one chunk) is 512 contiguous bytes, and a
 // transposed read (8 rows x 4 chunks x 8 bytes) hits every bank exactly twice; all inner-loop
 // addresses are a per-lane base plus a constant.
+#include <type_traits>
+
 #include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
@@ -36,7 +38,6 @@ namespace dc {
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int R, int D>
 struct CMTile {
@@ -188,10 +189,12 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         fill_cm<kKM, D, VEC>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, kKW, cnt, lane);
         fill_cm<kKM, D, VEC>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, kKW, cnt, lane);
     };
-    // lse (+inf past L: P = 0 there) and dsum of a step, one value per lane of waves 0 and 1.
+    // -lse log2 e (-inf past L: P = 0 there) and dsum of a step, one value per lane of waves
+    // 0 and 1.  (The float32 kernels subtract lse in natural-log units first, which saves one
+    // rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
     auto load_row_stat = [&](int i) -> float {
         const int bh = step_bh(i), qq = step_m0(i) + lane;
-        if (wave == 0) return qq < s.L ? a.lse[(int64_t)bh * s.L + qq] : INFINITY;
+        if (wave == 0) return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e : -INFINITY;
         return qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
     };
     auto store_row_stat = [&](int i, float x) {
@@ -224,9 +227,10 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         }
 
         const int mq = m0 + 32 * qh;  // this wave's 32 queries
+        const u32x4 *qt = sm.m.q[buf], *ot = sm.m.o[buf];
+        const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
         const bool live = kw0 < s.S && mq < s.L && (!CAUSAL || mq + 31 >= kw0);
         if (live) {
-            const u32x4 *qt = sm.m.q[buf], *ot = sm.m.o[buf];
             f32x16 sacc, pacc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
@@ -237,27 +241,35 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                 pacc = mfma_bf16(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
                                  row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
             }
-
-            const bool edge = kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > mq);
-            const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
+            // P and dS; EDGE (keys past S or crossing the diagonal) is a separate
+            // instantiation so that the common path carries no per-element masking.
+            auto elementwise = [&](auto edge_c) {
+                constexpr bool EDGE = decltype(edge_c)::value;
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int row0 = 32 * qh + 8 * r4 + 4 * g;  // rows of registers 4 r4 .. 4 r4 + 3
-                const f32x4 ls = *reinterpret_cast<const f32x4 *>(&sm.m.lse[buf][row0]);
-                const f32x4 dsm = *reinterpret_cast<const f32x4 *>(&sm.m.dsum[buf][row0]);
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int row0 = 32 * qh + 8 * r4 + 4 * g;  // rows of registers 4 r4 .. 4 r4 + 3
+                    const f32x4 nl = *reinterpret_cast<const f32x4 *>(&sm.m.lse[buf][row0]);
+                    const f32x4 dsm = *reinterpret_cast<const f32x4 *>(&sm.m.dsum[buf][row0]);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = 4 * r4 + j, qq = m0 + row0 + j;
-                    // scale * q.k (+ mask) - lse in natural-log units, as the reference forms
-                    // it, then one conversion to base 2.
-                    float x = sacc[r] * s.scale;
-                    if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-                    float p = exp2_fast((x - ls[j]) * kLog2e);
-                    if (edge && (key >= s.S || (CAUSAL && key > qq))) p = 0.f;
-                    sacc[r] = p;
-                    pacc[r] = p * (pacc[r] - dsm[j]);
+                    for (int j = 0; j < 4; ++j) {
+                        const int r = 4 * r4 + j, qq = m0 + row0 + j;
+                        // exponent in base 2: scale q.k (+ mask) - lse, times log2 e
+                        float x;
+                        if (MASK) {
+                            const float mk = (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+                            x = fmaf(fmaf(sacc[r], s.scale, mk), kLog2e, nl[j]);
+                        } else {
+                            x = fmaf(sacc[r], s.scale_log2, nl[j]);
+                        }
+                        if (EDGE && (key >= s.S || (CAUSAL && key > qq))) x = -INFINITY;
+                        const float p = exp2_fast(x);
+                        sacc[r] = p;
+                        pacc[r] = p * (pacc[r] - dsm[j]);
+                    }
                 }
-            }
+            };
+            if (kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > mq)) elementwise(std::true_type{});
+            else elementwise(std::false_type{});
 
             // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA.
 #pragma unroll
@@ -392,6 +404,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         }
     }
     const float lse_q = qi < s.L ? a.lse[(int64_t)bh * s.L + qi] : 0.f;
+    // -lse in base 2.  (The float32 kernels subtract lse in natural-log units first, which
+    // saves one rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
+    const float nlse2 = -lse_q * kLog2e;
     const float dsum_q = qi < s.L ? a.dsum[(int64_t)bh * s.L + qi] : 0.f;
     const float *mrow = nullptr;
     if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
@@ -452,15 +467,25 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                 sacc = mfma_bf16(row_frag<kQN, D>(kt_, rowb, 32 * kt, st), qreg[st], sacc);
                 pacc = mfma_bf16(row_frag<kQN, D>(vt_, rowb, 32 * kt, st), oreg[st], pacc);
             }
+            // dS^T; EDGE (keys past S or past the diagonal) is a separate instantiation so
+            // that the common path carries no per-element masking.
+            auto elementwise = [&](auto edge_c) {
+                constexpr bool EDGE = decltype(edge_c)::value;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = n0 + kt * 32 + acc_row(r, g);
-                float x = sacc[r] * s.scale;
-                if (MASK) x += mv[kt][r];
-                float p = exp2_fast((x - lse_q) * kLog2e);
-                if (edge && (key >= s.S || (CAUSAL && key > qi))) p = 0.f;
-                sacc[r] = p * (pacc[r] - dsum_q);  // dS^T
-            }
+                for (int r = 0; r < 16; ++r) {
+                    // exponent in base 2: scale q.k (+ mask) - lse, times log2 e
+                    float x;
+                    if (MASK) x = fmaf(fmaf(sacc[r], s.scale, mv[kt][r]), kLog2e, nlse2);
+                    else x = fmaf(sacc[r], s.scale_log2, nlse2);
+                    if (EDGE) {
+                        const int key = n0 + kt * 32 + acc_row(r, g);
+                        if (key >= s.S || (CAUSAL && key > qi)) x = -INFINITY;
+                    }
+                    sacc[r] = exp2_fast(x) * (pacc[r] - dsum_q);
+                }
+            };
+            if (edge) elementwise(std::true_type{});
+            else elementwise(std::false_type{});
             // dQ^T += K^T dS^T, 16 keys per MFMA.
 #pragma unroll
             for (int u = 0; u < 2; ++u) {

@@ -49,14 +49,27 @@ DEVI float xor32_add(float x) { return x + __shfl_xor(x, 32, 64); }
 DEVI float bf16_to_f32(__bf16 x) { return static_cast<float>(x); }
 DEVI __bf16 f32_to_bf16(float x) { return static_cast<__bf16>(x); }  // round to nearest even
 
-// x[at + j] (j = 0..7) as hi + lo with hi = bf16(x) and lo = bf16(x - hi).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two float32 values rounded to nearest bf16, packed low/high (one v_cvt_pk_bf16_f32).
+DEVI uint32_t cvt_pk_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
+// x[at + j] (j = 0..7) as hi + lo with hi = bf16(x) and lo = bf16(x - hi), converted in pairs:
+// 6 VALU operations per pair (two packed conversions, two unpacks, two subtractions).
 DEVI void split_bf16(const f32x16 &x, int at, bf16x8 &hi, bf16x8 &lo) {
+    u32x4 h, l;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const __bf16 h = static_cast<__bf16>(x[at + j]);
-        hi[j] = h;
-        lo[j] = static_cast<__bf16>(x[at + j] - static_cast<float>(h));
+    for (int w = 0; w < 4; ++w) {
+        const float x0 = x[at + 2 * w], x1 = x[at + 2 * w + 1];
+        h[w] = cvt_pk_bf16(x0, x1);
+        l[w] = cvt_pk_bf16(x0 - __uint_as_float(h[w] << 16), x1 - __uint_as_float(h[w] & 0xffff0000u));
     }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
 }
 
 template <typename T> DEVI float to_f32(T x);
