@@ -241,6 +241,8 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                 pacc = mfma_bf16(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
                                  row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
             }
+            // Keep the operand reads (two per MFMA) four MFMAs ahead of their use.
+            sched_reads_ahead<2 * KSTEP, 2, 4>();
             // P and dS; EDGE (keys past S or crossing the diagonal) is a separate
             // instantiation so that the common path carries no per-element masking.
             auto elementwise = [&](auto edge_c) {
@@ -467,6 +469,8 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                 sacc = mfma_bf16(row_frag<kQN, D>(kt_, rowb, 32 * kt, st), qreg[st], sacc);
                 pacc = mfma_bf16(row_frag<kQN, D>(vt_, rowb, 32 * kt, st), oreg[st], pacc);
             }
+            // Keep the operand reads (one per MFMA) four MFMAs ahead of their use.
+            sched_reads_ahead<2 * KSTEP, 1, 4>();
             // dS^T; EDGE (keys past S or past the diagonal) is a separate instantiation so
             // that the common path carries no per-element masking.
             auto elementwise = [&](auto edge_c) {

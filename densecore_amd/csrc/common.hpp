@@ -94,6 +94,20 @@ DEVI void lds_dma16(const void *src, void *dst) {
 // s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
 DEVI void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// Scheduling hint for a straight run of NMFMA MFMAs, each consuming R LDS reads issued in the
+// same block: the reads are kept AHEAD MFMAs in front of their use (the compiler otherwise
+// issues each read just before its MFMA and exposes the LDS latency on every one).
+template <int NMFMA, int R, int AHEAD>
+DEVI void sched_reads_ahead() {
+    __builtin_amdgcn_sched_group_barrier(0x100, R * AHEAD, 0);  // DS reads
+#pragma unroll
+    for (int i = 0; i < NMFMA - AHEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+}
+
 // Launches `kernel` and returns the status of this launch alone (hipGetLastError would also
 // report errors left behind by unrelated earlier calls in the process).
 template <typename... Params, typename... Args>

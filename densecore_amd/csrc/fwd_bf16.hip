@@ -215,11 +215,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
         if (live[NT - 1]) {
-            // Every sub-tile live: their independent MFMA chains are interleaved.
+            // Every sub-tile live: their independent MFMA chains are interleaved, with the K
+            // fragment reads kept four MFMAs ahead (the compiler would otherwise issue each
+            // read just before its MFMA and expose the LDS latency every time).
 #pragma unroll
             for (int st = 0; st < KSTEP; ++st)
 #pragma unroll
                 for (int kt = 0; kt < NT; ++kt) sacc[kt] = mfma_bf16(kfrag(kt, st), qreg[st], sacc[kt]);
+            sched_reads_ahead<KSTEP * NT, 1, 4>();
         } else {
             // One uniform test per sub-tile, outside its chain.
 #pragma unroll
