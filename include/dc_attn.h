@@ -45,7 +45,7 @@ extern "C" {
 typedef enum {
     DC_OK = 0,
     DC_INVALID_ARGUMENT = 1, /* shape / argument errors: the reference raises ValueError */
-    DC_UNSUPPORTED = 2,      /* outside what the kernels implement (e.g. E > 256) */
+    DC_UNSUPPORTED = 2,      /* outside what the kernels implement (e.g. E > 128) */
     DC_EXECUTION_FAILED = 3  /* a HIP launch or runtime error: the reference's RuntimeError */
 } dc_status;
 
