@@ -41,6 +41,11 @@ def _offset_causal(rows, keys, a):
     (2, 2, 2, 7, 7, 5, False), (1, 3, 3, 33, 33, 16, True), (1, 2, 2, 100, 37, 12, False),
     (1, 1, 1, 200, 200, 64, True), (2, 4, 2, 300, 300, 128, True), (1, 2, 1, 129, 257, 128, False),
     (1, 2, 2, 64, 64, 32, True), (2, 2, 2, 190, 190, 100, True),
+    # one query (three keys: with one key dq is exactly 0 and the relative bar would compare
+    # rounding noise), L > S and L < S under causal masking, 4 query heads per kv head, head
+    # dim 1 (every tile of every kernel is partial)
+    (1, 1, 1, 1, 3, 64, False), (1, 2, 2, 1, 300, 64, False), (1, 2, 2, 300, 100, 64, True),
+    (1, 2, 2, 100, 300, 64, True), (1, 4, 1, 70, 70, 64, True), (2, 2, 2, 40, 40, 1, True),
 ])
 def test_bf16_shapes(oracle_lib, B, H, Hkv, L, S, E, causal):
     from densecore_amd import _native
@@ -129,3 +134,47 @@ def test_c5_windows(oracle_lib, c5_run, a, b):
     if b == d["q"].shape[2]:
         assert_bf16(sel(res["dk"], slice(a, b)), rk[:, :, a:], f"C5 dk[{a}:]")
         assert_bf16(sel(res["dv"], slice(a, b)), rv[:, :, a:], f"C5 dv[{a}:]")
+
+
+def _bf_misaligned(x):
+    """A contiguous bf16 device copy of x whose data pointer is 2 bytes past a 16-byte boundary."""
+    x = np.ascontiguousarray(x, np.float32)
+    flat = torch.empty(x.size + 8, dtype=torch.bfloat16, device=DEV)
+    view = flat[1:1 + x.size].view(x.shape)
+    view.copy_(torch.from_numpy(x).to(DEV).to(torch.bfloat16))
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+@pytest.mark.parametrize("E", [32, 64, 128])
+def test_bf16_unaligned_pointers(oracle_lib, E):
+    """Inputs not 16-byte aligned take the element-wise tile fills (no global_load_lds) of the
+    forward, dK/dV and dQ kernels at head dims equal to the instantiated ones."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(300 + E)
+    B, H, L, E_ = 1, 2, 150, E
+    q, k, v, g = (bf16_round(rng.standard_normal((B, H, L, E_), dtype=np.float32)) for _ in range(4))
+    print(f"[case] bf16 unaligned E{E}", flush=True)
+    tq, tk, tv, tg = (_bf_misaligned(x) for x in (q, k, v, g))
+    out, lse = _native._flash_attention(tq, tk, tv, True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    assert_bf16(_np(out), ref_o, "out")
+    assert_bf16(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), True)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, True)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_bf16(_np(a), b, name)
+
+
+def test_bf16_backward_bit_reproducible():
+    """The bf16 backward has no atomics: two runs give bit-identical dq, dk and dv."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(11)
+    q, k, v, g = (_bf(bf16_round(rng.standard_normal((2, 4, 700, 128), dtype=np.float32)))
+                  for _ in range(4))
+    out, lse = _native._flash_attention(q, k, v, True)
+    first = _native._flash_attention_backward(g, q, k, v, out, lse, True)
+    second = _native._flash_attention_backward(g, q, k, v, out, lse, True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), first, second):
+        assert torch.equal(a, b), name

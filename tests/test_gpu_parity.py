@@ -202,3 +202,35 @@ def test_golden_fixtures(tag):
     got = _run_bwd(g, q, k, v, z[f"{tag}/out"], z[f"{tag}/lse"], bool(causal), scale, mask)
     for name, a in zip(("dq", "dk", "dv"), got):
         assert_f32(a, z[f"{tag}/{name}"], f"{tag} {name}")
+
+
+def _misaligned(x):
+    """A contiguous float32 device copy of x whose data pointer is 4 bytes past a 16-byte
+    boundary."""
+    x = np.ascontiguousarray(x, np.float32)
+    flat = torch.empty(x.size + 4, dtype=torch.float32, device=DEV)
+    view = flat[1:1 + x.size].view(x.shape)
+    view.copy_(torch.from_numpy(x).to(DEV))
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+@pytest.mark.parametrize("E", [32, 64, 128])
+def test_unaligned_pointers(oracle_lib, E):
+    """Inputs not 16-byte aligned take the element-wise load paths of the forward and backward
+    kernels at head dims equal to the instantiated ones."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(400 + E)
+    q, k, v, g = (rng.standard_normal((1, 2, 150, E), dtype=np.float32) for _ in range(4))
+    print(f"[case] fp32 unaligned E{E}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    out, lse = _native._flash_attention(_misaligned(q), _misaligned(k), _misaligned(v), True)
+    torch.cuda.synchronize()
+    assert_f32(out.cpu().numpy(), ref_o, "unaligned out")
+    assert_f32(lse.cpu().numpy(), ref_l, "unaligned lse")
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, True)
+    got = _native._flash_attention_backward(_misaligned(g), _misaligned(q), _misaligned(k),
+                                            _misaligned(v), _misaligned(ref_o), _t(ref_l), True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_f32(a.cpu().numpy(), b, f"unaligned {name}")
