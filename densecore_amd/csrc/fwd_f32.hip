@@ -25,9 +25,7 @@
 namespace dc {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 32 * kWaves;
+// W waves per workgroup, 32 queries per wave (4, or 2 for short causal problems).
 
 template <int D, int BN>
 struct alignas(16) FwdSmem {
@@ -36,8 +34,9 @@ struct alignas(16) FwdSmem {
 };
 
 // Global -> register staging of one K/V tile (fast path: E == D, 16-byte aligned rows).
-template <int D, int BN>
+template <int D, int BN, int W>
 struct KVStage {
+    static constexpr int kThreads = 64 * W;
     static constexpr int C4 = D / 4;
     static constexpr int N = BN * C4 / kThreads;
     static_assert(BN * C4 % kThreads == 0, "tile must split evenly over the workgroup");
@@ -67,10 +66,10 @@ struct KVStage {
 };
 
 // Generic path: any E <= D, any alignment; loads straight into LDS.
-template <int D, int BN>
+template <int D, int BN, int W>
 DEVI void load_kv_generic(FwdSmem<D, BN> &sm, const float *kb, const float *vb, int n0, int S,
                           int E, int tid) {
-    for (int i = tid; i < BN * D; i += kThreads) {
+    for (int i = tid; i < BN * D; i += 64 * W) {
         const int r = i / D, c = i % D, key = n0 + r;
         const bool ok = key < S && c < E;
         sm.k[r][c] = ok ? kb[(int64_t)key * E + c] : 0.f;
@@ -99,12 +98,12 @@ DEVI int swz(int row) {
 
 // Issue this wave's share of tile [n0, n0 + BN) into buffer `buf` (keys past the end read a
 // valid row, S - 1; their scores are -inf, so they contribute nothing).
-template <int D, int BN>
+template <int D, int BN, int W>
 DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, int n0, int S,
                      int wave, int lane) {
     constexpr int C = D / 4;             // 16-byte chunks per row
     constexpr int RPL = 64 / C;          // rows per wave-wide load
-    constexpr int ROWS = BN / kWaves;    // rows per wave
+    constexpr int ROWS = BN / W;         // rows per wave
     static_assert(ROWS % RPL == 0, "a wave loads whole rows");
 #pragma unroll
     for (int j = 0; j < ROWS / RPL; ++j) {
@@ -117,8 +116,9 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
     }
 }
 
-template <int D, int BN, bool CAUSAL, bool MASK, bool ASYNC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
+template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
+    constexpr int kThreads = 64 * W, kBM = 32 * W;
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
     constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
     using Smem = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, FwdSmem<D, BN>>::type;
@@ -173,9 +173,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     const int kv_end = CAUSAL ? min(q0 + kBM, s.S) : s.S;
     const int ntiles = (kv_end + BN - 1) / BN;
 
-    KVStage<D, BN> stage;
+    KVStage<D, BN, W> stage;
     if constexpr (ASYNC) {
-        if (ntiles > 0) issue_tile<D, BN>(sm, kb, vb, 0, s.S, wave, lane);
+        if (ntiles > 0) issue_tile<D, BN, W>(sm, kb, vb, 0, s.S, wave, lane);
     } else if (s.vec && ntiles > 0) {
         stage.load(kb, vb, 0, s.S, tid);
     }
@@ -187,13 +187,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         if constexpr (ASYNC) {
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile t landed
             __syncthreads();  // everyone's loads landed; everyone is done with tile t - 1
-            if (t + 1 < ntiles) issue_tile<D, BN>(nxt, kb, vb, n0 + BN, s.S, wave, lane);
+            if (t + 1 < ntiles) issue_tile<D, BN, W>(nxt, kb, vb, n0 + BN, s.S, wave, lane);
         } else {
             __syncthreads();  // everyone is done reading the previous tile
             if (s.vec) {
                 stage.store(cur, tid);
             } else {
-                load_kv_generic<D, BN>(cur, kb, vb, n0, s.S, s.E, tid);
+                load_kv_generic<D, BN, W>(cur, kb, vb, n0, s.S, s.E, tid);
             }
             __syncthreads();
             if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
@@ -359,28 +359,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     }
 }
 
-template <int D, int BN>
+template <int D, int BN, int W>
 hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     FwdArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked alignment; E must fill D
-    const int nqt = (a.s.L + kBM - 1) / kBM;
-    const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
+    const int nqt = (a.s.L + 32 * W - 1) / (32 * W);
+    const dim3 grid(nqt * a.s.B * a.s.H), block(64 * W);
     const bool mask = a.s.mask != nullptr;
     if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
-            return_if(launch(fwd_f32_kernel<D, BN, true, false, true>, grid, block, st, a));
+            return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a));
         else if (mask)
-            return_if(launch(fwd_f32_kernel<D, BN, false, true, true>, grid, block, st, a));
+            return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true>, grid, block, st, a));
         else
-            return_if(launch(fwd_f32_kernel<D, BN, false, false, true>, grid, block, st, a));
+            return_if(launch(fwd_f32_kernel<D, BN, W, false, false, true>, grid, block, st, a));
     } else if (a.s.causal && mask) {
-        return_if(launch(fwd_f32_kernel<D, BN, true, true, false>, grid, block, st, a));
+        return_if(launch(fwd_f32_kernel<D, BN, W, true, true, false>, grid, block, st, a));
     } else if (a.s.causal) {
-        return_if(launch(fwd_f32_kernel<D, BN, true, false, false>, grid, block, st, a));
+        return_if(launch(fwd_f32_kernel<D, BN, W, true, false, false>, grid, block, st, a));
     } else if (mask) {
-        return_if(launch(fwd_f32_kernel<D, BN, false, true, false>, grid, block, st, a));
+        return_if(launch(fwd_f32_kernel<D, BN, W, false, true, false>, grid, block, st, a));
     } else {
-        return_if(launch(fwd_f32_kernel<D, BN, false, false, false>, grid, block, st, a));
+        return_if(launch(fwd_f32_kernel<D, BN, W, false, false, false>, grid, block, st, a));
     }
     return hipSuccess;
 }
@@ -389,9 +389,14 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
 
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st) {
     if (a.s.B == 0 || a.s.H == 0 || a.s.L == 0) return hipSuccess;
-    if (a.s.E <= 32) return launch_d<32, 64>(a, st);
-    if (a.s.E <= 64) return launch_d<64, 64>(a, st);
-    return launch_d<128, 32>(a, st);
+    // Short causal problems: 2-wave workgroups over 32-key tiles (four workgroups per CU).
+    // Their causal work units are finer, which balances the CUs better (measured on one MI355X:
+    // B64 H6 L256 D64 causal 54.0 -> 49.5 us; B8 H12 L1024 unchanged; non-causal B16 H16 L512
+    // slower, 161 -> 171 us).
+    const bool small = a.s.causal && a.s.L <= 256;
+    if (a.s.E <= 32) return small ? launch_d<32, 32, 2>(a, st) : launch_d<32, 64, 4>(a, st);
+    if (a.s.E <= 64) return small ? launch_d<64, 32, 2>(a, st) : launch_d<64, 64, 4>(a, st);
+    return launch_d<128, 32, 4>(a, st);
 }
 
 }  // namespace dc
