@@ -118,7 +118,8 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
 
 template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
-    constexpr int kThreads = 64 * W, kBM = 32 * W;
+    [[maybe_unused]] constexpr int kThreads = 64 * W;
+    constexpr int kBM = 32 * W;
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
     constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
     using Smem = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, FwdSmem<D, BN>>::type;
