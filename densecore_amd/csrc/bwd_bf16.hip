@@ -33,94 +33,10 @@
 #include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
+#include "tile_bf16.hpp"
 
 namespace dc {
 namespace {
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-template <int R, int D>
-struct CMTile {
-    static constexpr int C = D / 8;        // 16-byte chunks per row
-    static constexpr int P = R + 4;        // slots per chunk (4 pad slots)
-    static constexpr int SLOTS = C * P;
-    static constexpr int NI = (SLOTS + 63) / 64;  // wave-wide transfers per tile
-    static constexpr int CS = P * 16;      // chunk stride, bytes
-};
-
-// Transfers first, first + step, ... (count of them) of a chunk-major tile holding rows
-// [0, nrows) of `src` (row stride E elements); rows past nrows and dims past E are zero.
-template <int R, int D, bool VEC>
-DEVI void fill_cm(u32x4 *dst, const __bf16 *src, int nrows, int E, int first, int step,
-                  int count, int lane) {
-    using T = CMTile<R, D>;
-#pragma unroll
-    for (int j = 0; j < count; ++j) {
-        const int inst = first + step * j;
-        if (inst >= T::NI) break;  // wave-uniform
-        const int slot = inst * 64 + lane;
-        const int chunk = slot / T::P, row = slot % T::P;
-        if (slot >= T::SLOTS || row >= R) continue;
-        if (VEC && row < nrows) {
-            lds_dma16(src + (int64_t)row * D + chunk * 8, dst + inst * 64);
-        } else if (VEC) {
-            dst[slot] = u32x4{0u, 0u, 0u, 0u};
-        } else {
-            uint16_t h[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int d = chunk * 8 + e;
-                h[e] = (row < nrows && d < E) ? __builtin_bit_cast(uint16_t, src[(int64_t)row * E + d])
-                                              : (uint16_t)0;
-            }
-            u32x4 x;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) x[w] = (uint32_t)h[2 * w] | ((uint32_t)h[2 * w + 1] << 16);
-            dst[slot] = x;
-        }
-    }
-}
-
-// Row fragment (MFMA operand with rows on lanes): rows row0 + (l % 32), dims 16 st + 8 (l / 32)
-// + 0..7.  `lanebase` = (l % 32) * 16 + (l / 32) * CS.
-template <int R, int D>
-DEVI bf16x8 row_frag(const u32x4 *tile, uint32_t lanebase, int row0, int st) {
-    using T = CMTile<R, D>;
-    const char *p = reinterpret_cast<const char *>(tile) + lanebase + row0 * 16 + 2 * st * T::CS;
-    return *reinterpret_cast<const bf16x8 *>(p);
-}
-
-// Transposed fragment (MFMA operand with dims on lanes): dim 32 dt + (l % 32), rows
-// row0 + {4g..4g+3, 8+4g..8+4g+3} (g = l / 32), read by two ds_read_b64_tr_b16.
-// `lanebase` = (4g + (i >> 2)) * 16 + 8 (i & 1) + (2 half + ((i & 3) >> 1)) * CS, i = l % 16,
-// half = (l / 16) % 2.
-template <int R, int D>
-DEVI bf16x8 tr_frag(const u32x4 *tile, uint32_t lanebase, int row0, int dt) {
-    using T = CMTile<R, D>;
-    const char *p = reinterpret_cast<const char *>(tile) + lanebase + row0 * 16 + 4 * dt * T::CS;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(p));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4 *)(p + 8 * 16));
-    const s16x4 cat[2] = {lo, hi};
-    return __builtin_bit_cast(bf16x8, cat);
-}
-
-template <int R, int D>
-DEVI uint32_t row_lanebase(int lane) {
-    return (uint32_t)((lane & 31) * 16 + (lane >> 5) * CMTile<R, D>::CS);
-}
-template <int R, int D>
-DEVI uint32_t tr_lanebase(int lane) {
-    const int i = lane & 15, half = (lane >> 4) & 1, g = lane >> 5;
-    return (uint32_t)((4 * g + (i >> 2)) * 16 + 8 * (i & 1) + (2 * half + ((i & 3) >> 1)) * CMTile<R, D>::CS);
-}
-
-// Logical block index: blocks are dealt to the 8 XCDs round-robin, so consecutive logical
-// indices are spread to land on the same XCD (whose L2 then holds their shared K/V or Q/dO).
-DEVI int logical_block() {
-    const int n = gridDim.x, w = blockIdx.x;
-    return (n & 7) == 0 ? (w & 7) * (n >> 3) + (w >> 3) : w;
-}
 
 // ---------------------------------------------------------------------------------------
 // dK / dV (keys stationary)
@@ -135,10 +51,10 @@ struct alignas(16) DkdvSmem {
     using TK = CMTile<kKN, D>;
     using TQ = CMTile<kKM, D>;
     struct Main {
-        u32x4 k[TK::NI * 64];
-        u32x4 v[TK::NI * 64];
-        u32x4 q[2][TQ::NI * 64];
-        u32x4 o[2][TQ::NI * 64];
+        u32x4 k[TK::SLOTS];
+        u32x4 v[TK::SLOTS];
+        u32x4 q[2][TQ::SLOTS];
+        u32x4 o[2][TQ::SLOTS];
         float lse[2][kKM];
         float dsum[2][kKM];
     };
@@ -154,8 +70,6 @@ struct alignas(16) DkdvSmem {
 
 template <int D, bool CAUSAL, bool MASK, bool VEC>
 __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
-    using TK = CMTile<kKN, D>;
-    using TQ = CMTile<kKM, D>;
     constexpr int KSTEP = D / 16, NDT = D / 32;
     __shared__ DkdvSmem<D> sm;
 
@@ -173,8 +87,8 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)bhk * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)bhk * s.S * s.E;
     const int nkeys = min(kKN, s.S - n0);
-    fill_cm<kKN, D, VEC>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, kKW, (TK::NI + kKW - 1) / kKW, lane);
-    fill_cm<kKN, D, VEC>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, kKW, (TK::NI + kKW - 1) / kKW, lane);
+    fill_cm<kKN, D, VEC, kKW>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
+    fill_cm<kKN, D, VEC, kKW>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
 
     const int m_begin = CAUSAL ? n0 : 0;  // n0 is a multiple of kKM
     const int per_head = s.L > m_begin ? (s.L - m_begin + kKM - 1) / kKM : 0;
@@ -185,9 +99,8 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         const int bh = step_bh(i), m0 = step_m0(i), buf = i & 1;
         const int rows = min(kKM, s.L - m0);
         const int64_t off = ((int64_t)bh * s.L + m0) * s.E;
-        constexpr int cnt = (TQ::NI + kKW - 1) / kKW;
-        fill_cm<kKM, D, VEC>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, kKW, cnt, lane);
-        fill_cm<kKM, D, VEC>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, kKW, cnt, lane);
+        fill_cm<kKM, D, VEC, kKW>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, lane);
+        fill_cm<kKM, D, VEC, kKW>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, lane);
     };
     // -lse log2 e (-inf past L: P = 0 there) and dsum of a step, one value per lane of waves
     // 0 and 1.  (The float32 kernels subtract lse in natural-log units first, which saves one
@@ -359,13 +272,12 @@ constexpr int kQN = 64;        // keys per tile
 template <int D>
 struct alignas(16) DqSmem {
     using T = CMTile<kQN, D>;
-    u32x4 k[2][T::NI * 64];
-    u32x4 v[2][T::NI * 64];
+    u32x4 k[2][T::SLOTS];
+    u32x4 v[2][T::SLOTS];
 };
 
 template <int D, bool CAUSAL, bool MASK, bool VEC>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(BwdArgs a) {
-    using T = CMTile<kQN, D>;
     constexpr int KSTEP = D / 16, NDT = D / 32, NT = kQN / 32;
     __shared__ DqSmem<D> sm;
 
@@ -421,11 +333,10 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
     const int kv_end = CAUSAL ? min(q0 + kQM, s.S) : s.S;
     const int ntiles = (kv_end + kQN - 1) / kQN;
-    constexpr int cnt = (T::NI + kQW - 1) / kQW;
     auto fill = [&](int t) {
         const int n0 = t * kQN, rows = min(kQN, s.S - n0);
-        fill_cm<kQN, D, VEC>(sm.k[t & 1], kb + (int64_t)n0 * s.E, rows, s.E, wave, kQW, cnt, lane);
-        fill_cm<kQN, D, VEC>(sm.v[t & 1], vb + (int64_t)n0 * s.E, rows, s.E, wave, kQW, cnt, lane);
+        fill_cm<kQN, D, VEC, kQW>(sm.k[t & 1], kb + (int64_t)n0 * s.E, rows, s.E, wave, lane);
+        fill_cm<kQN, D, VEC, kQW>(sm.v[t & 1], vb + (int64_t)n0 * s.E, rows, s.E, wave, lane);
     };
     if (ntiles > 0) fill(0);
     const uint32_t rowb = row_lanebase<kQN, D>(lane);

@@ -91,6 +91,19 @@ DEVI void lds_dma16(const void *src, void *dst) {
                  : "memory", "m0");
 }
 
+// The same transfer addressed as a wave-uniform 64-bit base (held in SGPRs) plus a per-lane
+// 32-bit byte offset (the saddr form of the instruction), so a caller whose lane offsets do not
+// change between transfers spends no VALU on addresses.
+DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    const uint64_t sbase = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) << 32) |
+                           __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t m = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m), "v"(off), "s"(sbase)
+                 : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
 DEVI void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 

@@ -8,18 +8,16 @@
 //
 //   * 4 waves x 32 queries per workgroup; queries stay in VGPRs as bf16x8 B operands of
 //     S^T = K Q^T (keys x queries), so the softmax state is per lane;
-//   * K and V tiles of 64 keys are double-buffered in LDS in their natural [key][d] layout and
-//     filled by global_load_lds_dwordx4 while the previous tile is computed (no VGPR staging);
-//   * O^T += V^T P^T takes V^T straight from the [key][d] tile with ds_read_b64_tr_b16 (each
-//     16-lane group reads a 4-key x 16-dim block and gets it transposed: lane j of the group
-//     receives element j % 4 of the 8 bytes read by lanes j / 4, 4 + j / 4, 8 + j / 4 and
-//     12 + j / 4), and P straight from the S^T accumulator (the MFMA reduction index is
-//     permuted to the accumulator's row order: registers 8u..8u+7 of a lane in half g hold
-//     keys 16u + {4g..4g+3, 8+4g..8+4g+3});
-//   * LDS rows are padded instead of swizzled, so every address in the inner loop is a base
-//     plus a constant: K rows are D/8 + 1 16-byte chunks apart (an odd count: ds_read_b128 of
-//     16 consecutive rows hits 16 different bank groups) and V rows D/8 + 4 chunks apart (the
-//     eight rows of one transposed read fall into four different 64-byte bank groups);
+//   * K and V tiles of 64 keys are double-buffered in LDS, chunk-major (16-byte chunk c of
+//     key r at slot c * 68 + r), and filled by global_load_lds_dwordx4 while the previous tile
+//     is computed: no VGPR staging, and every transfer of a full tile has the same per-lane
+//     offset, so the fill costs no VALU work;
+//   * S^T reads 32 consecutive keys of one chunk per half-wave (512 contiguous bytes), and
+//     O^T += V^T P^T takes V^T straight from the same layout with ds_read_b64_tr_b16 (each
+//     16-lane group reads a 4-key x 16-dim block and gets it transposed), and P straight from
+//     the S^T accumulator (the MFMA reduction index is permuted to the accumulator's row
+//     order: registers 8u..8u+7 of a lane in half g hold keys 16u + {4g..4g+3,
+//     8+4g..8+4g+3}); every address in the inner loop is a per-lane base plus a constant;
 //   * the running max moves only when a tile's max exceeds it by more than 8 (base 2), so the
 //     output accumulator is rarely rescaled;
 //   * workgroups are ordered (batch*head)-major, longest causal tile first, and spread so that
@@ -27,6 +25,7 @@
 //     round-robin), which keeps its K/V in that XCD's L2.
 #include "common.hpp"
 #include "params.hpp"
+#include "tile_bf16.hpp"
 
 namespace dc {
 namespace {
@@ -36,64 +35,23 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;  // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <int D>
-struct TileGeom {
-    static constexpr int C = D / 8;                    // 16-byte chunks per row
-    static constexpr int KS = C + 1;                   // K row stride, chunks
-    static constexpr int VS = C % 8 == 0 ? C + 4 : C;  // V row stride, chunks
-    static constexpr int KSLOTS = kBN * KS, VSLOTS = kBN * VS;
-    static constexpr int KI = (KSLOTS + 63) / 64, VI = (VSLOTS + 63) / 64;  // wave-wide transfers
-    static constexpr int KIW = (KI + kWaves - 1) / kWaves, VIW = (VI + kWaves - 1) / kWaves;
-};
-
-// One K/V tile: padded rows of bf16 as 16-byte chunks.
+// One K/V tile pair (chunk-major, 64 keys).
 template <int D>
 struct alignas(16) KVTileBf16 {
-    u32x4 k[TileGeom<D>::KI * 64];
-    u32x4 v[TileGeom<D>::VI * 64];
+    u32x4 k[CMTile<kBN, D>::SLOTS];
+    u32x4 v[CMTile<kBN, D>::SLOTS];
 };
 
-// Fill `t` with keys [n0, n0 + kBN): slot s of a matrix holds chunk s % stride of row
-// s / stride; pad slots are skipped, rows past S are zero.
+// Fill `t` with keys [n0, n0 + kBN); keys past S are zero.
 template <int D, bool VEC>
 DEVI void fill_tile(KVTileBf16<D> &t, const __bf16 *kb, const __bf16 *vb, int n0, int S, int E,
                     int wave, int lane) {
-    using G = TileGeom<D>;
-    auto one = [&](u32x4 *dst, const __bf16 *src, int stride, int nslots, int j) {
-        const int inst = wave + kWaves * j;
-        const int slot = inst * 64 + lane;
-        const int row = slot / stride, chunk = slot % stride, key = n0 + row;
-        if (slot >= nslots || chunk >= G::C) return;
-        if (VEC && key < S) {
-            lds_dma16(src + (int64_t)key * D + chunk * 8, dst + inst * 64);
-        } else if (VEC) {
-            dst[slot] = u32x4{0u, 0u, 0u, 0u};
-        } else {
-            uint16_t h[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int d = chunk * 8 + e;
-                h[e] = (key < S && d < E) ? __builtin_bit_cast(uint16_t, src[(int64_t)key * E + d])
-                                          : (uint16_t)0;
-            }
-            u32x4 x;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) x[w] = (uint32_t)h[2 * w] | ((uint32_t)h[2 * w + 1] << 16);
-            dst[slot] = x;
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < G::KIW; ++j) one(t.k, kb, G::KS, G::KSLOTS, j);
-#pragma unroll
-    for (int j = 0; j < G::VIW; ++j) one(t.v, vb, G::VS, G::VSLOTS, j);
+    fill_cm<kBN, D, VEC, kWaves>(t.k, kb + (int64_t)n0 * E, S - n0, E, wave, lane);
+    fill_cm<kBN, D, VEC, kWaves>(t.v, vb + (int64_t)n0 * E, S - n0, E, wave, lane);
 }
 
 template <int D, bool CAUSAL, bool MASK, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(FwdArgs a) {
-    using G = TileGeom<D>;
     constexpr int NT = kBN / 32;  // 32-key sub-tiles per tile
     constexpr int KSTEP = D / 16; // MFMA k-steps over the head dim
     constexpr int NDT = D / 32;   // 32-dim output tiles
@@ -155,11 +113,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int ntiles = (kv_end + kBN - 1) / kBN;
     if (ntiles > 0) fill_tile<D, VEC>(sm[0], kb, vb, 0, s.S, s.E, wave, lane);
 
-    // Byte offsets of this lane's fragments inside a tile: K for S^T (row lr, dims 8g..),
-    // V for the transposed read (row 4g + (i >> 2), dims 16 * half + 4 (i & 3)).
-    const int i16 = lane & 15, half = (lane >> 4) & 1;
-    const uint32_t koff = (uint32_t)(lr * G::KS * 16 + g * 16);
-    const uint32_t voff = (uint32_t)((4 * g + (i16 >> 2)) * G::VS * 16 + (16 * half + 4 * (i16 & 3)) * 2);
+    const uint32_t rowb = row_lanebase<kBN, D>(lane);
+    const uint32_t trb = tr_lanebase<kBN, D>(lane);
 
     auto tile = [&](int t) {
         const int n0 = t * kBN;
@@ -168,20 +123,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         __syncthreads();       // everyone's landed; everyone is done with tile t - 1
         if (t + 1 < ntiles) fill_tile<D, VEC>(sm[(t + 1) & 1], kb, vb, n0 + kBN, s.S, s.E, wave, lane);
 
-        const char *kbase = reinterpret_cast<const char *>(cur.k) + koff;
-        const char *vbase = reinterpret_cast<const char *>(cur.v) + voff;
-        auto kfrag = [&](int kt, int st) {
-            return *reinterpret_cast<const bf16x8 *>(kbase + kt * 32 * G::KS * 16 + st * 32);
-        };
-        auto vfrag = [&](int kt, int u, int dt) {
-            const char *p = vbase + (kt * 32 + 16 * u) * G::VS * 16 + dt * 64;
-            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) s16x4 *)(p));
-            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) s16x4 *)(p + 8 * G::VS * 16));
-            const s16x4 cat[2] = {lo, hi};
-            return __builtin_bit_cast(bf16x8, cat);
-        };
+        // K rows kt * 32 + (l % 32) for S^T; V^T (dims on lanes) for keys 16u + {4g..4g+3,
+        // 8+4g..8+4g+3} of sub-tile kt, the rows P's accumulator registers 8u..8u+7 hold.
+        auto kfrag = [&](int kt, int st) { return row_frag<kBN, D>(cur.k, rowb, kt * 32, st); };
+        auto vfrag = [&](int kt, int u, int dt) { return tr_frag<kBN, D>(cur.v, trb, kt * 32 + 16 * u, dt); };
 
         bool live[NT];
 #pragma unroll
