@@ -95,9 +95,12 @@ DEVI void lds_dma16(const void *src, void *dst) {
 // 32-bit byte offset (the saddr form of the instruction), so a caller whose lane offsets do not
 // change between transfers spends no VALU on addresses.
 DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
+    // readfirstlane returns int: each half goes back to uint32_t before widening, or a low
+    // half with bit 31 set would sign-extend over the high half.
     const uint64_t p = (uint64_t)(uintptr_t)base;
-    const uint64_t sbase = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) << 32) |
-                           __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    const uint64_t sbase = ((uint64_t)hi << 32) | lo;
     const uint32_t m = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m), "v"(off), "s"(sbase)

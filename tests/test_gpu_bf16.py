@@ -166,6 +166,38 @@ def test_bf16_unaligned_pointers(oracle_lib, E):
         assert_bf16(_np(a), b, name)
 
 
+def test_bf16_high_half_addresses(oracle_lib):
+    """Inputs whose addresses have bit 31 set in their low 32 bits: the tile fills split each
+    tile's base address into two 32-bit halves (scalar registers), and the low half must be
+    widened without sign extension.  The tensors are in-bounds views into one 4.1 GiB
+    buffer, placed so that every one of them starts 3 GiB into a 4 GiB window."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(31)
+    B, H, L, E = 1, 2, 300, 128
+    xs = [bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(4)]
+    n = B * H * L * E
+    buf = torch.empty((1 << 31) + 4 * n + 64, dtype=torch.bfloat16, device=DEV)
+    target = 3 << 30  # low 32 bits of the first tensor's address
+    off = ((target - buf.data_ptr()) % (1 << 32)) // 2  # in elements; data_ptr is 256-aligned
+    views = []
+    for i, x in enumerate(xs):
+        v = buf[off + i * n: off + (i + 1) * n].view(B, H, L, E)
+        v.copy_(_bf(x))
+        assert v.data_ptr() % 16 == 0 and (v.data_ptr() & 0xFFFFFFFF) >= 1 << 31
+        views.append(v)
+    tq, tk, tv, tg = views
+    q, k, v, g = xs
+    print("[case] bf16 high-half addresses", flush=True)
+    out, lse = _native._flash_attention(tq, tk, tv, True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    assert_bf16(_np(out), ref_o, "out")
+    assert_bf16(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), True)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, True)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_bf16(_np(a), b, name)
+
+
 def test_bf16_backward_bit_reproducible():
     """The bf16 backward has no atomics: two runs give bit-identical dq, dk and dv."""
     from densecore_amd import _native
