@@ -32,9 +32,10 @@ constexpr int kBM = 32;           // queries per step
 
 template <int D>
 struct alignas(16) BwdSmem {
-    // K rows, read by the dQ product with lanes along d and four keys per step: a row stride
-    // of D + 16 words puts the four key rows of one read in different 16-bank windows.
-    float k[kBN][D + 16];
+    // K^T (row d holds the tile's keys), read by the dQ product as four consecutive keys per
+    // lane: with a row stride of kBN + 4 words the 16 rows of one ds_read_b128 start 4 banks
+    // apart.
+    float kt[D][kBN + 4];
     float q[kBM][D + 4];         // read along d with ds_read_b128 per lane: padded rows
     float dout[kBM][D + 4];
     float ds[kBM][kBN + 4];      // dS of the step, all four waves' keys
@@ -99,26 +100,51 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
 }
 
 // dQ[m0 .. m0+31][:] += scale * dS K for the step whose dS is in sm.ds.  The 32 x D tile is
-// split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32 over `nkeys` keys: lane l
-// supplies A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element
-// gets exactly one global atomic per workgroup step.
+// split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32: lane l supplies
+// A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element gets exactly
+// one global atomic per workgroup step.  The reduction index is permuted so that a lane's four
+// steps over a 16-key block take four consecutive keys: step u of block kb gives lane l key
+// 16 kb + 4 (l/16) + u, and its dS and K^T operands for the block are one ds_read_b128 each.
+// Keys are covered in whole blocks up to nkeys rounded up to 16; the extra keys lie in the
+// same 32-key wave group as key nkeys - 1, whose dS columns this step wrote (zeros past S).
 template <int D>
 DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L, int E,
                      float scale, int wave, int lane) {
     constexpr int TPW = D / 32;
+    constexpr int NB = kBN / 16;  // 16-key blocks in a full tile
     const int r16 = lane & 15, c4 = lane >> 4;
     const int qh = wave >> 1, dbase = (wave & 1) * (D / 2);
+    const float *arow = &sm.ds[qh * 16 + r16][4 * c4];
+    const float *brow = &sm.kt[dbase + r16][4 * c4];
+    constexpr int BSTRIDE = 16 * (kBN + 4);  // words between the wave's 16 x 16 output blocks
     f32x4 acc[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int steps = (nkeys + 3) / 4;
-#pragma unroll 4
-    for (int st = 0; st < steps; ++st) {
-        const float av = sm.ds[qh * 16 + r16][4 * st + c4];
+    auto block = [&](int kb) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(arow + 16 * kb);
+        f32x4 b4[TPW];
 #pragma unroll
-        for (int j = 0; j < TPW; ++j)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                av, sm.k[4 * st + c4][dbase + 16 * j + r16], acc[j], 0, 0, 0);
+        for (int j = 0; j < TPW; ++j) b4[j] = *reinterpret_cast<const f32x4 *>(brow + j * BSTRIDE + 16 * kb);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < TPW; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[u], b4[j][u], acc[j], 0, 0, 0);
+    };
+    const int nblk = (nkeys + 15) >> 4;
+    if (nblk == NB) {
+        // Whole tile: unrolled, each block's reads issued one block ahead of its MFMAs.
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) block(kb);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1 + TPW, 0);
+#pragma unroll
+        for (int kb = 0; kb < NB - 1; ++kb) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1 + TPW, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * TPW, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * TPW, 0);
+    } else {
+        for (int kb = 0; kb < nblk; ++kb) block(kb);
     }
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
@@ -131,7 +157,7 @@ DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L,
     }
 }
 
-template <int D, bool CAUSAL, bool MASK>
+template <int D, bool CAUSAL, bool MASK, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
     constexpr int DH = D / 2;
     constexpr int NDT = D / 32;
@@ -154,7 +180,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     float kreg[DH], vreg[DH];
     {
         const float *kr = kb + (int64_t)key * s.E, *vr = vb + (int64_t)key * s.E;
-        if (s.vec && key < s.S) {
+        if (VEC && key < s.S) {
 #pragma unroll
             for (int t = 0; t < DH; t += 4) {
                 const f32x4 x = *reinterpret_cast<const f32x4 *>(kr + g * DH + t);
@@ -172,10 +198,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             }
         }
     }
-    // The workgroup's K tile in LDS, for the dQ product.
-    for (int i = tid; i < kBN * D; i += kThreads) {
-        const int r = i / D, c = i % D, kk = n0 + r;
-        sm.k[r][c] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
+    // The workgroup's K tile, transposed into LDS for the dQ product (lanes along keys, so
+    // the LDS writes are conflict-free).
+    if (VEC) {
+        for (int i = tid; i < kBN * (D / 4); i += kThreads) {
+            const int r = i % kBN, c = (i / kBN) * 4, kk = n0 + r;
+            const f32x4 x = kk < s.S ? *reinterpret_cast<const f32x4 *>(kb + (int64_t)kk * D + c)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sm.kt[c + u][r] = x[u];
+        }
+    } else {
+        for (int i = tid; i < kBN * D; i += kThreads) {
+            const int r = i % kBN, c = i / kBN, kk = n0 + r;
+            sm.kt[c][r] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
+        }
     }
 
     f32x16 dk[NDT], dv[NDT];
@@ -196,7 +233,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
 
     QStage<D> stage;
-    if (s.vec && nsteps > 0) {
+    if (VEC && nsteps > 0) {
         const int bh = step_head(0);
         stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
                    static_cast<const float *>(a.dout) + (int64_t)bh * s.L * D,
@@ -209,7 +246,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         if (prev_bh >= 0)
             dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0),
                           s.L, s.E, s.scale, wave, lane);
-        if (s.vec) {
+        if (VEC) {
             stage.store(sm, tid);
         } else {
             stage_generic<D>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
@@ -217,7 +254,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
                              a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
         }
         __syncthreads();  // the tile is staged and the previous dQ product has read sm.ds
-        if (s.vec && i + 1 < nsteps) {
+        if (VEC && i + 1 < nsteps) {
             const int nbh = step_head(i + 1);
             stage.load(static_cast<const float *>(a.q) + (int64_t)nbh * s.L * D,
                        static_cast<const float *>(a.dout) + (int64_t)nbh * s.L * D,
@@ -291,7 +328,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
             for (int r = 0; r < 16; r += 4) {
                 const int d = dt * 32 + acc_row(r, g);
-                if (s.vec) {
+                if (VEC) {
                     *reinterpret_cast<f32x4 *>(dkr + d) =
                         f32x4{dk[dt][r] * s.scale, dk[dt][r + 1] * s.scale,
                               dk[dt][r + 2] * s.scale, dk[dt][r + 3] * s.scale};
@@ -309,22 +346,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     }
 }
 
-template <int D>
-hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
-    BwdArgs a = args;
-    a.s.vec = args.s.vec && args.s.E == D;
+template <int D, bool VEC>
+hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     const int nkt = (a.s.S + kBN - 1) / kBN;
     const dim3 grid(nkt * a.s.B * a.s.Hkv), block(kThreads);
     const bool mask = a.s.mask != nullptr;
-    if (a.s.causal && mask)
-        return_if(launch(bwd_f32_kernel<D, true, true>, grid, block, st, a));
-    else if (a.s.causal)
-        return_if(launch(bwd_f32_kernel<D, true, false>, grid, block, st, a));
-    else if (mask)
-        return_if(launch(bwd_f32_kernel<D, false, true>, grid, block, st, a));
-    else
-        return_if(launch(bwd_f32_kernel<D, false, false>, grid, block, st, a));
-    return hipSuccess;
+    if (a.s.causal && mask) return launch(bwd_f32_kernel<D, true, true, VEC>, grid, block, st, a);
+    if (a.s.causal) return launch(bwd_f32_kernel<D, true, false, VEC>, grid, block, st, a);
+    if (mask) return launch(bwd_f32_kernel<D, false, true, VEC>, grid, block, st, a);
+    return launch(bwd_f32_kernel<D, false, false, VEC>, grid, block, st, a);
+}
+
+template <int D>
+hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
+    BwdArgs a = args;
+    a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked 16-byte alignment; E must fill D
+    return a.s.vec ? launch_dv<D, true>(a, st) : launch_dv<D, false>(a, st);
 }
 
 }  // namespace
