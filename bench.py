@@ -7,8 +7,9 @@ C2 (the headline) is causal fp32 forward + backward at
 D64 through the C ABI (dc_sdpa_fwd then dc_sdpa_bwd).  ``value`` is C2's algorithmic TFLOP/s
 (4*B*H*T^2*D/2 forward, 2.5x that backward).  The same line carries the decode figure the
 metric names (C4, dc_sdpa_decode, GB/s of K + V + q + out + lse), the other configurations'
-throughput, a roofline entry per kernel family timed with HIP events on the launch stream,
-and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
+throughput (wall clock over K steps between two synchronizations), a roofline entry per
+entry point whose kernel time comes from HIP events on the launch stream around back-to-back
+calls of that entry point alone, and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
 """
 import argparse
 import json
@@ -48,23 +49,17 @@ def load_traffic():
     return {}
 
 
-class Timer:
-    """Accumulates HIP-event durations of calls made on one stream."""
-
-    def __init__(self, torch, stream):
-        self.torch, self.stream, self.pairs = torch, stream, []
-
-    def __call__(self, fn):
-        t = self.torch
-        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        a.record(self.stream)
-        r = fn()
-        b.record(self.stream)
-        self.pairs.append((a, b))
-        return r
-
-    def mean_ms(self):
-        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs])) if self.pairs else 0.0
+def kernel_ms(torch, stream, fn, n):
+    """Average duration of one call of ``fn`` (its kernels only, launched back to back) from one
+    pair of HIP events around n calls on the launch stream.  An event pair around every call
+    would add two marker packets, and their waits, to each call's time."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(n):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / n
 
 
 def roofline(achieved, peak, unit, bound, traffic, kernel, work_note):
@@ -87,31 +82,35 @@ def bench_prefill(torch, native, name, steps, warmup, dev):
         mask = torch.from_numpy(additive(d["mask_bool"], (B, 1, 1, S)).copy()).to(dev).expand(B, H, L, S)
     scale = 1.0 / np.sqrt(E)
     stream = torch.cuda.current_stream(dev)
-    tf, tb = Timer(torch, stream), Timer(torch, stream)
 
-    def step(timed):
-        if timed:
-            out, lse = tf(lambda: native._flash_attention(q, k, v, causal, scale, mask))
-            if bwd:
-                tb(lambda: native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask))
-        else:
-            out, lse = native._flash_attention(q, k, v, causal, scale, mask)
-            if bwd:
-                native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask)
+    def fwd():
+        return native._flash_attention(q, k, v, causal, scale, mask)
+
+    def step():
+        out, lse = fwd()
+        if bwd:
+            native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask)
 
     for _ in range(warmup):
-        step(False)
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step(True)
+        step()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
+    # Per-entry-point kernel time, for the roofline: the same calls, back to back.
+    n = max(steps, 10)
+    res = {"ms_per_step": wall, "fwd_ms": kernel_ms(torch, stream, fwd, n), "bwd_ms": 0.0,
+           "timing_calls": n}
+    if bwd:
+        out, lse = fwd()
+        res["bwd_ms"] = kernel_ms(torch, stream, lambda: native._flash_attention_backward(
+            g, q, k, v, out, lse, causal, scale, mask), n)
     ff, fb = flops(B, H, L, S, E, causal, bwd)
     if name == "C3":  # useful work counts valid keys only
         ff = 4.0 * H * L * E * float(np.sum(d["lengths"]))
-    res = {"ms_per_step": wall, "fwd_ms": tf.mean_ms(), "bwd_ms": tb.mean_ms(),
-           "fwd_flop": ff, "bwd_flop": fb}
+    res.update({"fwd_flop": ff, "bwd_flop": fb})
     res["tflops"] = (ff + fb) / (wall * 1e-3) / 1e12
     res["fwd_tflops"] = ff / (res["fwd_ms"] * 1e-3) / 1e12
     if bwd:
@@ -126,18 +125,18 @@ def bench_decode(torch, native, steps, warmup, dev):
     q, k, v = (torch.from_numpy(d[n]).to(dev) for n in "qkv")
     del d
     stream = torch.cuda.current_stream(dev)
-    t = Timer(torch, stream)
     for _ in range(warmup):
         native._flash_decode(q, k, v)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        t(lambda: native._flash_decode(q, k, v))
+        native._flash_decode(q, k, v)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
+    n = max(steps, 10)
+    ev = kernel_ms(torch, stream, lambda: native._flash_decode(q, k, v), n)
     nbytes = decode_bytes(B, H, S, E)
-    ev = t.mean_ms()
-    return {"ms_per_step": wall, "event_ms": ev, "bytes": nbytes,
+    return {"ms_per_step": wall, "event_ms": ev, "bytes": nbytes, "timing_calls": n,
             "gbps": nbytes / (ev * 1e-3) / 1e9}
 
 
@@ -219,21 +218,25 @@ def main():
         line["roofline"] = roofline(
             c2["bwd_tflops"], PEAK_FP32_MFMA, "TFLOP/s", "mfma", traffic.get("C2_bwd"),
             "dc_sdpa_bwd (bwd_pre_kernel + bwd_f32_kernel)",
-            f"{c2['bwd_flop'] / 1e9:.3f} GFLOP per call / {c2['bwd_ms']:.4f} ms (HIP events)")
+            f"{c2['bwd_flop'] / 1e9:.3f} GFLOP per call / {c2['bwd_ms']:.4f} ms (HIP events around "
+            f"{c2['timing_calls']} back-to-back calls)")
         line["forward_roofline"] = roofline(
             c2["fwd_tflops"], PEAK_FP32_MFMA, "TFLOP/s", "mfma", traffic.get("C2_fwd"),
             "dc_sdpa_fwd (fwd_f32_kernel)",
-            f"{c2['fwd_flop'] / 1e9:.3f} GFLOP per call / {c2['fwd_ms']:.4f} ms (HIP events)")
+            f"{c2['fwd_flop'] / 1e9:.3f} GFLOP per call / {c2['fwd_ms']:.4f} ms (HIP events around "
+            f"{c2['timing_calls']} back-to-back calls)")
         line["mfma_frac"] = round(c2["tflops"] / PEAK_FP32_MFMA, 4)
     c4 = results.get("C4")
     if c4:
         line["decode"] = {"workload": "C4: decode fp32, B=32 H=32 S=4096 D=128, split-KV",
                           "value": round(c4["gbps"], 1), "unit": "GB/s",
-                          "ms_per_step": round(c4["event_ms"], 4),
+                          "ms_per_step": round(c4["ms_per_step"], 4),
+                          "kernel_ms": round(c4["event_ms"], 4),
                           "roofline": roofline(c4["gbps"], PEAK_HBM, "GB/s", "hbm",
                                                traffic.get("C4_decode"),
                                                "dc_sdpa_decode (decode_split + decode_merge)",
-                                               f"{c4['bytes']} B per call / {c4['event_ms']:.4f} ms")}
+                                               f"{c4['bytes']} B per call / {c4['event_ms']:.4f} ms (HIP events "
+                                               f"around {c4['timing_calls']} back-to-back calls)")}
     others = {}
     for name in ("C1", "C3", "C5"):
         r = results.get(name)
