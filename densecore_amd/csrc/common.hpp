@@ -42,9 +42,18 @@ DEVI int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 DEVI float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 DEVI float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
 
-// Combine a value with the one held by lane l ^ 32 (the other half of the wave).
-DEVI float xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
-DEVI float xor32_add(float x) { return x + __shfl_xor(x, 32, 64); }
+// Combine a value with the one held by lane l ^ 32 (the other half of the wave) through
+// v_permlane32_swap (no LDS): the pair it returns holds, in every lane, the values of lanes
+// l % 32 and l % 32 + 32, in the same order in both halves, so both halves get bit-identical
+// results.
+DEVI float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+DEVI float xor32_add(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 DEVI float bf16_to_f32(__bf16 x) { return static_cast<float>(x); }
 DEVI __bf16 f32_to_bf16(float x) { return static_cast<__bf16>(x); }  // round to nearest even

@@ -269,18 +269,244 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
+// Unmasked variants: two groups of four waves ping-pong.  Waves w and w + 4 of a workgroup
+// share a SIMD; a SIMD overlaps one wave's MFMA work with another wave's VALU work, but not
+// the two within one wave.  So the workgroup runs in phases separated by barriers, and in
+// each phase one group runs its GEMM step while the other runs its softmax step:
+//   GEMM(t):     S(t) = K(t) Q^T (16 MFMAs) and O^T += V(t-1)^T P(t-1)^T (32 MFMAs);
+//   SOFTMAX(t):  edge masking, tile max, lazy rescale, P(t) = exp2(S(t) c - m), l += P, and
+//                P(t) split into its bf16 hi and lo halves for the next GEMM step.
+// Group 0 runs GEMM(0), SOFTMAX(0), GEMM(1), ... and group 1 the same one phase later.  Each
+// group owns 128 queries (the workgroup 256) and both read the same K/V tiles: K(t) is read in
+// phases 2t and 2t + 1, V(t) in phases 2t + 2 and 2t + 3; at every even phase 2s the waves
+// issue K(s + 1) and V(s) into the double buffers, and wait for them at the end of phase
+// 2s + 1.  A wave skips the steps (not the barriers or its share of the transfers) of tiles
+// whose keys all follow its last query.
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = 64 * kPPWaves;
+constexpr int kPPM = 32 * kPPWaves;  // queries per workgroup
+
+template <int D, bool CAUSAL, bool VEC>
+__global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_pp_kernel(FwdArgs a) {
+    constexpr int NT = kBN / 32, KSTEP = D / 16, NDT = D / 32;
+    __shared__ KVTileBf16<D> sm[2];
+
+    const AttnShape &s = a.s;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int nqt = (s.L + kPPM - 1) / kPPM;
+    const int w = logical_block();
+    const int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
+    const int q0 = qt * kPPM;
+    const int wave_q0 = q0 + grp * 128 + (wave & 3) * 32, wave_last_q = wave_q0 + 31;
+    const int qi = wave_q0 + lr;
+
+    const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+    const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+
+    const bool neg = s.scale_log2 < 0.f;
+    const float c = neg ? -s.scale_log2 : s.scale_log2;
+    bf16x8 qreg[KSTEP];
+    {
+        const __bf16 *qrow = static_cast<const __bf16 *>(a.q) + ((int64_t)bh * s.L + qi) * s.E;
+#pragma unroll
+        for (int t = 0; t < KSTEP; ++t) {
+            const int d0 = 16 * t + 8 * g;
+            if (VEC && qi < s.L) {
+                qreg[t] = *reinterpret_cast<const bf16x8 *>(qrow + d0);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    qreg[t][e] = (qi < s.L && d0 + e < s.E) ? qrow[d0 + e] : static_cast<__bf16>(0.f);
+            }
+            if (neg) {
+                u32x4 x = __builtin_bit_cast(u32x4, qreg[t]);
+                x ^= 0x80008000u;
+                qreg[t] = __builtin_bit_cast(bf16x8, x);
+            }
+        }
+    }
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+    float m_run = -INFINITY, l_part = 0.f;
+    f32x16 sc[NT];                // S(t), raw
+    bf16x8 ph[NT][2], pl[NT][2];  // P(t) as hi + lo, sub-tile kt, 16-key half u
+
+    const int kv_end = CAUSAL ? min(q0 + kPPM, s.S) : s.S;
+    const int ntiles = (kv_end + kBN - 1) / kBN;
+    const uint32_t rowb = row_lanebase<kBN, D>(lane);
+    const uint32_t trb = tr_lanebase<kBN, D>(lane);
+
+    auto fill_k = [&](int t) {
+        fill_cm<kBN, D, VEC, kPPWaves>(sm[t & 1].k, kb + (int64_t)t * kBN * s.E, s.S - t * kBN, s.E, wave, lane);
+    };
+    auto fill_v = [&](int t) {
+        fill_cm<kBN, D, VEC, kPPWaves>(sm[t & 1].v, vb + (int64_t)t * kBN * s.E, s.S - t * kBN, s.E, wave, lane);
+    };
+    // Sub-tile kt of tile t holds a key this wave's queries see.
+    auto sub_live = [&](int t, int kt) {
+        const int k0 = t * kBN + kt * 32;
+        return k0 < s.S && (!CAUSAL || k0 <= wave_last_q);
+    };
+
+    // PV(t-1) first, then S(t): P's registers are dead before S is written, so the two share
+    // registers.
+    auto gemm = [&](int t) {
+        if (t >= 1 && sub_live(t - 1, 0)) {
+            const u32x4 *vt_ = sm[(t - 1) & 1].v;
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                if (kt > 0 && !sub_live(t - 1, kt)) continue;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    bf16x8 va[NDT];
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt) va[dt] = tr_frag<kBN, D>(vt_, trb, kt * 32 + 16 * u, dt);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], ph[kt][u], oacc[dt]);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], pl[kt][u], oacc[dt]);
+                }
+            }
+        }
+        if (t < ntiles && sub_live(t, 0)) {
+            const u32x4 *kt_ = sm[t & 1].k;
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc[kt][r] = 0.f;
+#pragma unroll
+            for (int st = 0; st < KSTEP; ++st)
+#pragma unroll
+                for (int kt = 0; kt < NT; ++kt)
+                    sc[kt] = mfma_bf16(row_frag<kBN, D>(kt_, rowb, kt * 32, st), qreg[st], sc[kt]);
+            sched_reads_ahead<KSTEP * NT, 1, 4>();
+        }
+    };
+    // Keys past S or (causal) past the query get -inf; the exponent reference m_run moves (and O,
+    // l are rescaled) only when some lane's tile max exceeds it by more than 8, so P <= 2^8;
+    // out = O / l and lse = m_run + log2(l) are exact either way.
+    auto softmax = [&](int t) {
+        if (t >= ntiles || !sub_live(t, 0)) return;
+        const int n0 = t * kBN;
+        if (n0 + kBN > s.S || (CAUSAL && n0 + kBN - 1 > wave_q0)) {
+            // Register r of sub-tile kt holds key n0 + 32 kt + 4g + (8 (r/4) + r%4).
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                const int base = n0 + kt * 32 + 4 * g;
+                const int lim = min(s.S - base, CAUSAL ? qi - base + 1 : s.S - base);
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) >= lim) sc[kt][r] = -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kt][r]);
+        mx = xor32_max(mx) * c;
+        if (__any(mx > m_run + 8.f)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = exp2_fast(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_part *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = exp2_fast(fmaf(sc[kt][r], c, neg_m));
+                sc[kt][r] = p;
+                l_part += p;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) split_bf16(sc[kt], 8 * u, ph[kt][u], pl[kt][u]);
+        }
+    };
+
+    // fill(t) at phase 2t: K(t + 1) into K(t - 1)'s buffer, V(t) into V(t - 2)'s buffer.
+    auto fill = [&](int t) {
+        if (t + 1 < ntiles) fill_k(t + 1);
+        if (t < ntiles) fill_v(t);
+    };
+    if (ntiles > 0) fill_k(0);
+    if (VEC) wait_vmem();
+    __syncthreads();
+    // Phases 0 .. 2 ntiles + 1, one barrier each; the transfers issued at an even phase are
+    // waited for at the end of the next (odd) one.  Each group has its own loop, so that only
+    // the registers of S (group 1) or of P (group 0) are carried from one iteration to the next.
+    if (grp == 0) {
+        for (int t = 0; t <= ntiles; ++t) {
+            fill(t);
+            gemm(t);
+            __syncthreads();
+            softmax(t);
+            if (VEC) wait_vmem();
+            __syncthreads();
+        }
+    } else {
+        for (int t = 0; t <= ntiles; ++t) {
+            fill(t);
+            if (t >= 1) softmax(t - 1);
+            __syncthreads();
+            gemm(t);
+            if (VEC) wait_vmem();
+            __syncthreads();
+        }
+    }
+
+    const float l_run = xor32_add(l_part);
+    if (qi < s.L) {
+        const bool empty = l_run == 0.f;
+        const float inv = empty ? 0.f : 1.f / l_run;
+        __bf16 *orow = static_cast<__bf16 *>(a.out) + ((int64_t)bh * s.L + qi) * s.E;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+                const int d = dt * 32 + acc_row(r, g);
+                if (VEC) {
+                    const bf16x4 o = {static_cast<__bf16>(oacc[dt][r] * inv),
+                                      static_cast<__bf16>(oacc[dt][r + 1] * inv),
+                                      static_cast<__bf16>(oacc[dt][r + 2] * inv),
+                                      static_cast<__bf16>(oacc[dt][r + 3] * inv)};
+                    *reinterpret_cast<bf16x4 *>(orow + d) = o;
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (d + u < s.E) orow[d + u] = static_cast<__bf16>(oacc[dt][r + u] * inv);
+                }
+            }
+        if (g == 0)
+            a.lse[(int64_t)bh * s.L + qi] = empty ? 0.f : (m_run + log2_fast(l_run)) * kLn2;
+    }
+}
+
 template <int D, bool VEC>
 hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
+    const bool mask = a.s.mask != nullptr;
+    if (!mask) {
+        const int nqt = (a.s.L + kPPM - 1) / kPPM;
+        const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
+        if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC>, grid, block, st, a);
+        return launch(fwd_bf16_pp_kernel<D, false, VEC>, grid, block, st, a);
+    }
     const int nqt = (a.s.L + kBM - 1) / kBM;
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
-    const bool mask = a.s.mask != nullptr;
-    if (a.s.causal && mask)
-        return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
-    if (a.s.causal)
-        return launch(fwd_bf16_kernel<D, true, false, VEC>, grid, block, st, a);
-    if (mask)
-        return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
-    return launch(fwd_bf16_kernel<D, false, false, VEC>, grid, block, st, a);
+    if (a.s.causal) return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
+    return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
 }
 
 template <int D>
