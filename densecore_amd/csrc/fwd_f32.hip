@@ -116,7 +116,7 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
     }
 }
 
-template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC>
+template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC, bool ROWMASK = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     [[maybe_unused]] constexpr int kThreads = 64 * W;
     constexpr int kBM = 32 * W;
@@ -163,6 +163,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     }
     const float *mrow = nullptr;
     if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
+    // ROWMASK: the mask does not depend on the query (stride 0 along L, e.g. key padding).  Each
+    // wave then reads a tile's mask with one coalesced load (lane l: key n0 + l), a tile ahead,
+    // takes the sub-tiles' liveness from a ballot, and hands the values to the accumulator
+    // layout through its own 64-float LDS slot.
+    static_assert(!ROWMASK || (MASK && BN <= 64), "row masks: one value per lane and tile");
+    __shared__ float mslot[ROWMASK ? W : 1][64];
+    auto row_mask = [&](int t) -> float {
+        const int key = t * BN + lane;
+        return (ROWMASK && lane < BN && key < s.S) ? mrow[key] : -INFINITY;
+    };
+    float mask_next = 0.f;
 
     f32x16 oacc[D / 32];
 #pragma unroll
@@ -180,15 +191,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     } else if (s.vec && ntiles > 0) {
         stage.load(kb, vb, 0, s.S, tid);
     }
+    if constexpr (ROWMASK) mask_next = row_mask(0);
 
     // One tile per call; the asynchronous path alternates two distinct LDS objects so that
     // the compiler can see the in-flight loads never alias the tile being read.
-    auto tile = [&](int t, auto &cur, auto &nxt) {
+    // tn: the tile to stream in next (t + 1; -1: none).
+    auto tile = [&](int t, auto &cur, auto &nxt, int tn) {
         const int n0 = t * BN;
         if constexpr (ASYNC) {
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile t landed
-            __syncthreads();  // everyone's loads landed; everyone is done with tile t - 1
-            if (t + 1 < ntiles) issue_tile<D, BN, W>(nxt, kb, vb, n0 + BN, s.S, wave, lane);
+            __syncthreads();  // everyone's loads landed; everyone is done with the previous tile
+            if (tn >= 0) issue_tile<D, BN, W>(nxt, kb, vb, tn * BN, s.S, wave, lane);
         } else {
             __syncthreads();  // everyone is done reading the previous tile
             if (s.vec) {
@@ -224,7 +237,26 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
         // (query, key) of the wave is skipped like an invisible one (key padding): its
         // probabilities are exactly 0.  Queries past L count as fully masked.
         float mv[MASK ? NT : 1][16];
-        if constexpr (MASK) {
+        if constexpr (ROWMASK) {
+            const float mcur = mask_next;
+            if (tn >= 0) mask_next = row_mask(tn);
+            // Liveness from a ballot; the values reach the accumulator layout through the wave's
+            // LDS slot.
+            const uint64_t open = __ballot(mcur != -INFINITY);
+            float *slot = mslot[wave];
+            slot[lane] = mcur;
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt) {
+                live[kt] = live[kt] && ((open >> (32 * kt)) & 0xffffffffull) != 0;
+                // registers r = 4j .. 4j + 3 hold keys 32 kt + 8j + 4g + 0..3
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 x = *reinterpret_cast<const f32x4 *>(&slot[32 * kt + 8 * j + 4 * g]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mv[kt][4 * j + e] = x[e];
+                }
+            }
+        } else if constexpr (MASK) {
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) {
                 bool any_open = false;
@@ -329,11 +361,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     };
     if constexpr (ASYNC) {
         for (int t = 0; t < ntiles; t += 2) {
-            tile(t, sm, sm2);
-            if (t + 1 < ntiles) tile(t + 1, sm2, sm);
+            tile(t, sm, sm2, t + 1 < ntiles ? t + 1 : -1);
+            if (t + 1 < ntiles) tile(t + 1, sm2, sm, t + 2 < ntiles ? t + 2 : -1);
         }
     } else {
-        for (int t = 0; t < ntiles; ++t) tile(t, sm, sm);
+        for (int t = 0; t < ntiles; ++t) tile(t, sm, sm, -1);
     }
 
     if (qi < s.L) {
@@ -370,6 +402,8 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
             return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a));
+        else if (mask && a.s.msl == 0 && BN <= 64)
+            return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true, true>, grid, block, st, a));
         else if (mask)
             return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true>, grid, block, st, a));
         else

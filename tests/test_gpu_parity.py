@@ -90,6 +90,46 @@ def test_masked_shapes(oracle_lib, B, H, L, S, E, kind):
     _check(oracle_lib, q, k, v, g, False, None, full, tag=f"mask-{kind}{(B, H, L, S, E)}")
 
 
+@pytest.mark.parametrize("B,H,L,S,E,kind", [
+    (2, 3, 70, 300, 64, "padding"), (2, 2, 130, 257, 64, "holes"), (1, 4, 64, 200, 128, "holes"),
+    (2, 2, 100, 100, 32, "per_head"), (1, 2, 50, 129, 48, "holes"), (2, 1, 40, 64, 64, "closed"),
+])
+def test_row_broadcast_masks(oracle_lib, B, H, L, S, E, kind):
+    """Masks that do not depend on the query (a stride-0 view along L: key padding and the like)
+    take their own path in the float32 forward (one mask load per key and tile, sub-tile liveness
+    from a ballot).  Padding, random holes, per-head rows, a fully masked batch row ("closed":
+    out 0, lse 0), 32-key tiles (E = 128) and the unaligned generic path (E = 48)."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(B * 7 + H * 11 + L + S + E)
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, H, S, E), dtype=np.float32) for _ in range(2))
+    if kind == "padding":
+        lens = rng.integers(1, S + 1, size=B)
+        allowed = np.arange(S)[None, None, None, :] < lens[:, None, None, None]
+    elif kind == "holes":
+        allowed = rng.random((B, 1, 1, S)) > 0.6
+    elif kind == "per_head":
+        allowed = rng.random((1, H, 1, S)) > 0.5
+    else:
+        allowed = np.ones((B, 1, 1, S), bool)
+        allowed[0] = False
+    small = np.where(allowed, np.float32(0), np.float32(-np.inf)).astype(np.float32)
+    view = _t(small).expand(B, H, L, S)
+    assert view.stride(2) == 0
+    full = additive(allowed, (B, H, L, S))
+    print(f"[case] row mask {kind} q{q.shape} k{k.shape}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False, None, full)
+    out, lse = _native._flash_attention(_t(q), _t(k), _t(v), False, None, view)
+    torch.cuda.synchronize()
+    assert_f32(out.cpu().numpy(), ref_o, f"row-{kind} out")
+    assert_f32(lse.cpu().numpy(), ref_l, f"row-{kind} lse")
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, False, None, full)
+    got = _native._flash_attention_backward(_t(g), _t(q), _t(k), _t(v), _t(ref_o), _t(ref_l), False,
+                                            None, view)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_f32(a.cpu().numpy(), b, f"row-{kind} {name}")
+
+
 @pytest.mark.parametrize("mode", ["none", "causal", "bool", "float"])
 def test_attention_rank4(oracle_lib, mode):
     """tests/test_attention.py:12-39, rank-4 (2, 3, 4, 8) cases."""
