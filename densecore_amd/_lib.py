@@ -1,4 +1,4 @@
-"""ctypes binding of ``libdcattn.so`` (the C ABI in ``include/dc_attn.h``).
+"""ctypes binding of ``libdcattn.so`` (the C ABI in ``include/dc_attn.h`` and ``include/dc_math.h``).
 
 The library is built in-tree (``densecore_amd/libdcattn.so``) by ``densecore_amd.build``.
 If it is missing, every entry point raises: there is no CPU fallback on this path.
@@ -12,11 +12,12 @@ LIB_PATH = os.path.join(_HERE, "libdcattn.so")
 DC_OK, DC_INVALID_ARGUMENT, DC_UNSUPPORTED, DC_EXECUTION_FAILED = 0, 1, 2, 3
 DC_F32, DC_BF16 = 0, 1
 
-# Every symbol include/dc_attn.h declares.
+# Every symbol include/dc_attn.h and include/dc_math.h declare.
 EXPORTS = ("dc_abi_version", "dc_last_error",
            "dc_sdpa_fwd_workspace_size", "dc_sdpa_fwd",
            "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
-           "dc_sdpa_decode_workspace_size", "dc_sdpa_decode")
+           "dc_sdpa_decode_workspace_size", "dc_sdpa_decode",
+           "dc_softmax_fwd", "dc_softmax_bwd")
 
 
 class Desc(ctypes.Structure):
@@ -27,6 +28,14 @@ class Desc(ctypes.Structure):
                 ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("mask_stride_b", ctypes.c_int64), ("mask_stride_h", ctypes.c_int64),
                 ("mask_stride_l", ctypes.c_int64)]
+
+
+class SoftmaxDesc(ctypes.Structure):
+    """``dc_softmax_desc``."""
+    _fields_ = [("rows", ctypes.c_int64), ("width", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("q_len", ctypes.c_int64), ("mask_stride_b", ctypes.c_int64),
+                ("mask_stride_h", ctypes.c_int64), ("mask_stride_l", ctypes.c_int64),
+                ("safe", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 _lib = None
@@ -50,7 +59,11 @@ def lib():
         L.dc_sdpa_fwd.argtypes = [D, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_bwd.argtypes = [D, P, P, P, P, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_decode.argtypes = [D, P, P, P, P, P, P, SZ, P]
-        for name in ("dc_sdpa_fwd", "dc_sdpa_bwd", "dc_sdpa_decode"):
+        SD = ctypes.POINTER(SoftmaxDesc)
+        L.dc_softmax_fwd.argtypes = [SD, P, P, P, P]
+        L.dc_softmax_bwd.argtypes = [SD, P, P, P, P]
+        for name in ("dc_sdpa_fwd", "dc_sdpa_bwd", "dc_sdpa_decode", "dc_softmax_fwd",
+                     "dc_softmax_bwd"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -138,6 +138,63 @@ def _flash_decode(q, k, v, scale=None):
     return out, lse
 
 
+def _softmax_desc(rows, width, heads=1, q_len=1, mstrides=(0, 0, 0), safe=False):
+    return _lib.SoftmaxDesc(int(rows), int(width), int(heads), int(q_len), *map(int, mstrides),
+                            int(bool(safe)), 0)
+
+
+def _softmax(scores, mask=None, safe=False):
+    """``Tensor.softmax(-1)`` of float32 scores (``src/torch_softmax.rs:57-67``) with the math
+    path's additive mask and safe rows fused (``python/densecore/functional.py:330-337``).
+
+    ``scores`` is (..., L, S); ``mask`` is None or a float32 tensor broadcastable to it; it is
+    read through the strides of its broadcast view (a stride of 0 is never materialised).
+    """
+    if scores.device.type != "cuda" or scores.dtype != torch.float32:
+        raise ValueError("softmax takes a float32 tensor on the GPU")
+    if scores.dim() == 0:
+        raise ValueError("softmax axis out of range")
+    x = scores.contiguous()
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    y = torch.empty_like(x)
+    heads = q_len = 1
+    ms = (0, 0, 0)
+    m = None
+    if mask is not None:
+        m = mask.to(device=x.device, dtype=torch.float32).expand(*x.shape)
+        if width > 1 and m.stride(-1) != 1:
+            m = m.contiguous()
+        # A (B, H, L, S) view of the mask: the kernel addresses row (b, h, l) by strides.
+        lead = x.dim() - 2
+        if lead < 0:
+            m = m.reshape(1, 1, 1, width)
+        elif lead <= 2:
+            m = m[(None,) * (2 - lead)]
+        else:
+            m = m.reshape(-1, x.shape[-3], x.shape[-2], width)
+        heads, q_len = m.shape[1], m.shape[2]
+        ms = (m.stride(0), m.stride(1), m.stride(2))
+    d = _softmax_desc(rows, width, heads, q_len, ms, safe)
+    _lib.check(_lib.lib().dc_softmax_fwd(d, _ptr(x), _ptr(m), _ptr(y), _stream(x.device)))
+    return y
+
+
+def _softmax_backward(grad_y, y):
+    """``softmax_backward_lastdim`` (``src/torch_softmax.rs:90-97``): (g - sum(g * y)) * y."""
+    if tuple(grad_y.shape) != tuple(y.shape):
+        raise ValueError("softmax backward shapes do not match")
+    g, y = grad_y.contiguous(), y.contiguous()
+    if g.dtype != torch.float32 or y.dtype != torch.float32 or g.device != y.device:
+        raise ValueError("softmax backward takes float32 tensors on one GPU")
+    width = y.shape[-1] if y.dim() else 1
+    rows = y.numel() // width if width else 0
+    dx = torch.empty_like(y)
+    d = _softmax_desc(rows, width)
+    _lib.check(_lib.lib().dc_softmax_bwd(d, _ptr(g), _ptr(y), _ptr(dx), _stream(y.device)))
+    return dx
+
+
 def default_scale(head_dim):
     """``sdp::calculate_scale`` as the Python layer passes it (a double)."""
     return 1.0 / math.sqrt(head_dim) if head_dim else 1.0

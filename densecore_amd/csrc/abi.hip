@@ -1,4 +1,4 @@
-// The C ABI declared in include/dc_attn.h: argument checks with the reference's messages,
+// The C ABI declared in include/dc_attn.h and include/dc_math.h: argument checks with the reference's messages,
 // scale computation, workspace carving, and dispatch to the kernel launchers.
 //
 // Checks follow the reference boundary (src/lib.rs:555-580 attention_dims, :594-607
@@ -10,6 +10,7 @@
 #include <string>
 
 #include "dc_attn.h"
+#include "dc_math.h"
 #include "params.hpp"
 
 namespace {
@@ -93,6 +94,45 @@ size_t decode_ws(const dc::AttnShape &s) {
     int split_len = 0;
     const int splits = dc::decode_splits(s, &split_len);
     return round_up((size_t)s.B * s.H * splits * (s.E + 2) * sizeof(float));
+}
+
+
+// src/activation_dispatch.rs:7-16 (the reference's softmax shape errors) plus the mask's row
+// decomposition and this library's int32 column indexing.
+dc_status check_softmax(const dc_softmax_desc *d, const float *mask, dc::SoftmaxArgs *a) {
+    if (d == nullptr) return fail(DC_INVALID_ARGUMENT, "softmax descriptor is null");
+    if (d->rows < 0 || d->width < 0) return fail(DC_INVALID_ARGUMENT, "softmax shape is negative");
+    if (d->width == 0)
+        return fail(DC_INVALID_ARGUMENT, "softmax requires a nonempty reduction axis");
+    if (d->width > INT32_MAX) return fail(DC_UNSUPPORTED, "softmax row length exceeds 2^31 - 1");
+    if (d->rows > (int64_t)4 * ((int64_t)UINT32_MAX >> 1))
+        return fail(DC_UNSUPPORTED, "softmax row count exceeds 2^33");
+    *a = dc::SoftmaxArgs{};
+    a->rows = d->rows;
+    a->width = (int)d->width;
+    a->heads = 1;
+    a->q_len = 1;
+    a->safe = d->safe != 0;
+    if (mask != nullptr) {
+        if (d->heads <= 0 || d->q_len <= 0 || d->heads > INT32_MAX || d->q_len > INT32_MAX ||
+            d->rows % (d->heads * d->q_len) != 0)
+            return fail(DC_INVALID_ARGUMENT, "softmax mask rows must be (B, H, L) with rows == B*H*L");
+        if (d->mask_stride_b < 0 || d->mask_stride_h < 0 || d->mask_stride_l < 0)
+            return fail(DC_INVALID_ARGUMENT, "softmax mask strides must be non-negative");
+        a->mask = mask;
+        a->heads = (int)d->heads;
+        a->q_len = (int)d->q_len;
+        a->msb = d->mask_stride_b;
+        a->msh = d->mask_stride_h;
+        a->msl = d->mask_stride_l;
+    }
+    return ok();
+}
+
+bool softmax_vec(const dc::SoftmaxArgs &a, const void *p0, const void *p1, const void *p2) {
+    bool v = a.width % 4 == 0 && aligned16(p0) && aligned16(p1) && (p2 == nullptr || aligned16(p2));
+    if (a.mask) v = v && aligned16(a.mask) && a.msb % 4 == 0 && a.msh % 4 == 0 && a.msl % 4 == 0;
+    return v;
 }
 
 }  // namespace
@@ -197,6 +237,34 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
     a.part = static_cast<float *>(workspace);
     a.splits = dc::decode_splits(s, &a.split_len);
     return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
+}
+
+dc_status dc_softmax_fwd(const dc_softmax_desc *d, const float *x, const float *mask, float *y,
+                         void *stream) {
+    dc::SoftmaxArgs a;
+    dc_status st = check_softmax(d, mask, &a);
+    if (st != DC_OK) return st;
+    if (a.rows == 0) return ok();
+    if (x == nullptr || y == nullptr) return fail(DC_INVALID_ARGUMENT, "softmax got a null pointer");
+    a.a = x;
+    a.out = y;
+    return launched(dc::launch_softmax_fwd(a, softmax_vec(a, x, y, nullptr),
+                                           static_cast<hipStream_t>(stream)));
+}
+
+dc_status dc_softmax_bwd(const dc_softmax_desc *d, const float *grad_y, const float *y,
+                         float *grad_x, void *stream) {
+    dc::SoftmaxArgs a;
+    dc_status st = check_softmax(d, nullptr, &a);
+    if (st != DC_OK) return st;
+    if (a.rows == 0) return ok();
+    if (grad_y == nullptr || y == nullptr || grad_x == nullptr)
+        return fail(DC_INVALID_ARGUMENT, "softmax got a null pointer");
+    a.a = grad_y;
+    a.b = y;
+    a.out = grad_x;
+    return launched(dc::launch_softmax_bwd(a, softmax_vec(a, grad_y, y, grad_x),
+                                           static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

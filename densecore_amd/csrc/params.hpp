@@ -43,6 +43,18 @@ struct DecodeArgs {
     int splits, split_len;
 };
 
+// Row softmax (softmax.hip).
+struct SoftmaxArgs {
+    const float *a;    // forward: scores; backward: grad_y
+    const float *b;    // backward: y
+    float *out;        // forward: y; backward: grad_x
+    const float *mask;
+    int64_t rows;
+    int width, heads, q_len;
+    int64_t msb, msh, msl;
+    bool safe;
+};
+
 // Each launcher returns hipSuccess or the launch error; it never synchronizes.
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st);
 hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st);
@@ -50,6 +62,9 @@ hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs &a, bool bf16, hipStream_t st);
 int decode_splits(const AttnShape &s, int *split_len);
+// `vec`: rows (and mask rows) start 16-byte aligned and the width is a multiple of 4.
+hipError_t launch_softmax_fwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
+hipError_t launch_softmax_bwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
 
 // Largest head dim each kernel family instantiates.
 constexpr int kMaxHeadDim = 256;

@@ -7,15 +7,22 @@ attention is allowed and becomes 0 / -inf; a float mask is added), feeding the n
 ``_flash_attention`` / ``_flash_attention_backward`` pair through an autograd Function that
 saves (q, k, v, out, lse) for the backward.
 
+Inputs the flash path does not take (dropout, rank 3, Ev != E, masks the flash path rejects,
+float masks that require a gradient) go through the reference's math path
+(``functional.py:318-340``), composed on the device: the two batched products are the device
+BLAS (``torch.matmul``), the mask add, safe softmax and its gradient are this library's
+softmax kernels (``include/dc_math.h``).  ``multi_head_attention_forward``
+(``functional.py:400-461``) composes the same pieces.
+
 Differences, all on the device side of the boundary:
   * tensors are ``torch`` tensors on the GPU, float32 or bfloat16 (bf16 is new: the reference
-    flash path is float32 only, ``functional.py:314``);
+    flash path is float32 only, ``functional.py:314``); the math path is float32 only, as the
+    reference's is;
   * masks are passed as broadcast views, not materialised to (B, H, L, S) on the host;
-  * ``enable_gqa`` passes the kv heads straight to the kernels (they index kv head h // repeat,
-    as ``src/torch_attention.rs:159-167`` does) instead of widening K and V first;
-  * inputs that would take the reference's math path (dropout, rank 3, Ev != E, masks the
-    flash path rejects) raise ``NotImplementedError``: only the flash path is built here, and
-    there is no silent CPU or composed-op fallback.
+  * ``enable_gqa`` passes the kv heads straight to the flash kernels (they index kv head
+    h // repeat, as ``src/torch_attention.rs:159-167`` does) instead of widening K and V first;
+    the math path widens them as the reference does;
+  * nothing falls back to the CPU: an input no device path takes raises ``NotImplementedError``.
 """
 import math
 import numbers
@@ -61,10 +68,88 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
         flash_mask = _flash_mask(attn_mask, tuple(query.shape), source, query.device)
         if attn_mask is None or flash_mask is not None:
             return _flash_attention(query, key, value, is_causal, float(scale), flash_mask)
-    raise NotImplementedError(
-        "only DenseCore's flash path is built on the GPU (rank 4, no dropout, Ev == E, "
-        "float32/bfloat16, masks of shape (L|1, S|1) or (B|1, H|1, L|1, S|1)); "
-        "this call would take the reference's math path")
+    if gqa:
+        # Each kv head serves H // Hkv query heads (functional.py:287-293).
+        groups = query.shape[1] // key.shape[1]
+        key = key.repeat_interleave(groups, dim=1)
+        value = value.repeat_interleave(groups, dim=1)
+    return _math_attention(query, key, value, attn_mask, dropout_p, is_causal, float(scale))
+
+
+def _math_attention(query, key, value, attn_mask, dropout_p, is_causal, scale):
+    """PyTorch's math path as the reference composes it (``functional.py:318-340``): q and k^T
+    each scaled by sqrt(|scale|), one batched product, the additive mask, the safe softmax
+    (rows that are all -inf give 0), dropout, and the product with v."""
+    if any(t.dtype != torch.float32 for t in (query, key, value)):
+        raise NotImplementedError("the math attention path on the GPU takes float32 tensors "
+                                  "(the reference's math path is float32)")
+    if query.device.type != "cuda" or key.device != query.device or value.device != query.device:
+        raise ValueError("attention tensors must be on one GPU")
+    factor = math.sqrt(abs(scale))
+    q = query * float(-factor if scale < 0 else factor)
+    attn = torch.matmul(q, (key * float(factor)).transpose(-2, -1))
+    length, source = attn.shape[-2], attn.shape[-1]
+    if is_causal:
+        attn_mask = torch.ones((length, source), dtype=torch.bool, device=attn.device).tril()
+    additive = None
+    if attn_mask is not None:
+        if isinstance(attn_mask, torch.Tensor):
+            m = attn_mask.to(attn.device)
+        else:
+            m = torch.from_numpy(np.ascontiguousarray(np.asarray(attn_mask))).to(attn.device)
+        if m.dtype == torch.bool:
+            additive = torch.zeros(m.shape, dtype=torch.float32, device=attn.device).masked_fill_(
+                ~m, float("-inf"))
+        else:
+            additive = m if m.dtype == torch.float32 else m.float()
+    weights = softmax_masked(attn, additive, safe=additive is not None)
+    if dropout_p:
+        weights = dropout(weights, dropout_p, True)
+    return torch.matmul(weights, value)
+
+
+class _Softmax(torch.autograd.Function):
+    """Softmax over the last axis with the additive mask fused in; gradient
+    ``softmax_backward_lastdim`` (``src/torch_softmax.rs:90-97``).  A mask that requires a
+    gradient receives the scores' gradient summed over its broadcast dimensions, as the
+    reference's separate ``attn + additive`` would give it."""
+
+    @staticmethod
+    def forward(ctx, scores, mask, safe):
+        y = _native._softmax(scores, mask, safe)
+        ctx.save_for_backward(y)
+        ctx.mask_shape = None if mask is None else tuple(mask.shape)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad):
+        (y,) = ctx.saved_tensors
+        dx = _native._softmax_backward(grad, y)
+        dmask = None
+        if ctx.needs_input_grad[1]:
+            dmask = dx.sum_to_size(ctx.mask_shape) if ctx.mask_shape else dx.sum()
+        return dx, dmask, None
+
+
+def softmax_masked(scores, mask=None, safe=False):
+    """``softmax(scores + mask, -1)`` on the GPU; ``safe`` makes rows that are all -inf give 0
+    (the math path's ``_safe_softmax``, ``functional.py:334-337``)."""
+    return _Softmax.apply(scores, mask, bool(safe))
+
+
+def softmax(input, dim=-1):
+    """``Tensor.softmax`` over the last axis (``src/torch_softmax.rs:57-67``) for float32 GPU
+    tensors (other axes are moved last and back)."""
+    if dim < 0:
+        dim += input.dim()
+    if dim != input.dim() - 1:
+        return softmax(input.movedim(dim, -1), -1).movedim(-1, dim)
+    return _Softmax.apply(input, None, False)
+
+
+def dropout(input, p=0.5, training=True, generator=None):
+    """``functional.dropout`` (``python/densecore/functional.py:229-244``)."""
+    raise NotImplementedError("dropout on the GPU is not built yet")
 
 
 def _flash_mask(attn_mask, qshape, source, device):
@@ -119,3 +204,80 @@ def _flash_attention(query, key, value, causal, scale, mask=None):
 def flash_decode(query, key, value, scale=None):
     """One decode step: query (B, H, 1, E) against the whole KV cache (B, Hkv, S, E)."""
     return _native._flash_decode(query, key, value, None if scale is None else float(scale))[0]
+
+
+def _float_mask(mask):
+    """MHA masks (``functional.py:391-397``): a bool mask is True where attention is NOT
+    allowed (-inf); a float mask is added."""
+    if mask is None:
+        return None
+    if mask.dtype == torch.bool:
+        return torch.zeros(mask.shape, dtype=torch.float32, device=mask.device).masked_fill_(
+            mask, float("-inf"))
+    return mask
+
+
+def multi_head_attention_forward(query, key, value, embed_dim_to_check, num_heads, in_proj_weight,
+                                 in_proj_bias, bias_k, bias_v, add_zero_attn, dropout_p,
+                                 out_proj_weight, out_proj_bias, training=True,
+                                 key_padding_mask=None, need_weights=True, attn_mask=None,
+                                 use_separate_proj_weight=False, q_proj_weight=None,
+                                 k_proj_weight=None, v_proj_weight=None, static_k=None,
+                                 static_v=None, average_attn_weights=True, is_causal=False):
+    """PyTorch's reference algorithm as ``functional.py:400-461`` composes it, on the GPU.
+    Inputs are (L, N, E), or (L, E) unbatched.  ``is_causal`` is only a hint: ``attn_mask``
+    must still be given and is the one applied.  The projections and the two batched products
+    are device BLAS calls; the mask add and softmax (no safe rows here, as in the reference) are
+    this library's softmax kernel, and dropout its dropout."""
+    F = torch.nn.functional
+    if is_causal and attn_mask is None:
+        raise RuntimeError("Need attn_mask if specifying the is_causal hint")
+    batched = query.dim() == 3
+    if not batched:
+        query, key, value = query.unsqueeze(1), key.unsqueeze(1), value.unsqueeze(1)
+        if key_padding_mask is not None:
+            key_padding_mask = key_padding_mask.unsqueeze(0)
+    tgt_len, bsz, embed_dim = query.shape
+    if embed_dim != embed_dim_to_check:
+        raise ValueError(f"was expecting embedding dimension of {embed_dim_to_check}, but got {embed_dim}")
+    head_dim = embed_dim // num_heads
+    biases = (None, None, None) if in_proj_bias is None else in_proj_bias.chunk(3)
+    weights = ((q_proj_weight, k_proj_weight, v_proj_weight) if use_separate_proj_weight
+               else in_proj_weight.chunk(3))
+    q, k, v = (F.linear(x, w, b) for x, w, b in zip((query, key, value), weights, biases))
+    attn_mask = _float_mask(attn_mask)
+    if attn_mask is not None and attn_mask.dim() == 2:
+        attn_mask = attn_mask.unsqueeze(0)
+    key_padding_mask = _float_mask(key_padding_mask)
+    if bias_k is not None and bias_v is not None:
+        k = torch.cat([k, bias_k.expand(1, bsz, embed_dim)])
+        v = torch.cat([v, bias_v.expand(1, bsz, embed_dim)])
+        attn_mask = None if attn_mask is None else F.pad(attn_mask, (0, 1))
+        key_padding_mask = None if key_padding_mask is None else F.pad(key_padding_mask, (0, 1))
+    q = q.reshape(tgt_len, bsz * num_heads, head_dim).transpose(0, 1)
+    k = static_k if static_k is not None else k.reshape(k.shape[0], bsz * num_heads, head_dim).transpose(0, 1)
+    v = static_v if static_v is not None else v.reshape(v.shape[0], bsz * num_heads, head_dim).transpose(0, 1)
+    if add_zero_attn:
+        k = torch.cat([k, k.new_zeros(bsz * num_heads, 1, head_dim)], 1)
+        v = torch.cat([v, v.new_zeros(bsz * num_heads, 1, head_dim)], 1)
+        attn_mask = None if attn_mask is None else F.pad(attn_mask, (0, 1))
+        key_padding_mask = None if key_padding_mask is None else F.pad(key_padding_mask, (0, 1))
+    src_len = k.shape[1]
+    if key_padding_mask is not None:
+        padding = key_padding_mask.reshape(bsz, 1, 1, src_len).expand(bsz, num_heads, 1, src_len)
+        padding = padding.reshape(bsz * num_heads, 1, src_len)
+        attn_mask = padding if attn_mask is None else attn_mask + padding
+    scores = torch.bmm(q * math.sqrt(1.0 / head_dim), k.transpose(1, 2).contiguous())
+    probabilities = softmax_masked(scores, attn_mask, safe=False)
+    if training and dropout_p > 0:
+        probabilities = dropout(probabilities, dropout_p, True)
+    out = torch.bmm(probabilities, v).transpose(0, 1).reshape(tgt_len * bsz, embed_dim)
+    out = F.linear(out, out_proj_weight, out_proj_bias).reshape(tgt_len, bsz, -1)
+    if not batched:
+        out = out.squeeze(1)
+    if not need_weights:
+        return out, None
+    probabilities = probabilities.reshape(bsz, num_heads, tgt_len, src_len)
+    if average_attn_weights:
+        probabilities = probabilities.mean(1)
+    return out, probabilities if batched else probabilities.squeeze(0)

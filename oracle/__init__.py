@@ -186,3 +186,102 @@ def scale_factor(e, scale=None):
 
 def q_split(q_len):
     return int(lib().oracle_q_split(q_len))
+
+
+# ---- the math path's pieces (python/densecore/functional.py:318-340) ----
+
+def softmax(x):
+    """``softmax_lastdim`` (``src/torch_softmax.rs:57-67``) over the last axis."""
+    x = _f32(x)
+    width = x.shape[-1]
+    y = np.empty_like(x)
+    if x.size:
+        lib().oracle_softmax(_p(x), x.size // width, width, _p(y))
+    return y
+
+
+def softmax_backward(g, y):
+    """``softmax_backward_lastdim`` (``src/torch_softmax.rs:90-97``)."""
+    g, y = _f32(g), _f32(y)
+    width = y.shape[-1]
+    dx = np.empty_like(y)
+    if y.size:
+        lib().oracle_softmax_backward(_p(g), _p(y), y.size // width, width, _p(dx))
+    return dx
+
+
+def bmm(a, b, b_k_contiguous=False):
+    """``torch_blas::bmm`` (``src/torch_blas.rs:404-449``) over leading dims, float32.
+
+    Products with k*rows*cols >= 400 go through ``addmm`` to the Linux naive ``sgemm_``
+    (``src/torch_blas.rs:95-134``): each output is the float32 sum of rounded products in k
+    order.  Smaller ones take the plain loop of ``:414-442``: the first k - k % 4 products
+    rounded and added in order when k > 3 and both operands are contiguous along k (a is taken
+    as contiguous; ``b_k_contiguous`` says whether b is a transposed view), the rest fused
+    (emulated in float64: the product is exact there, then the sum is rounded once)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    rows, k = a.shape[-2], a.shape[-1]
+    cols = b.shape[-1]
+    lead = np.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    a = np.broadcast_to(a, lead + a.shape[-2:])
+    b = np.broadcast_to(b, lead + b.shape[-2:])
+    acc = np.zeros(lead + (rows, cols), np.float32)
+    small = k * rows * cols < 400
+    unfused = (k - k % 4 if (k > 3 and b_k_contiguous) else 0) if small else k
+    for t in range(k):
+        x = a[..., :, t][..., :, None]
+        y = b[..., t, :][..., None, :]
+        if t < unfused:
+            acc = acc + x * y
+        else:
+            acc = (acc.astype(np.float64) + x.astype(np.float64) * y.astype(np.float64)).astype(np.float32)
+    return acc
+
+
+def math_attention(query, key, value, attn_mask=None, is_causal=False, scale=None, noise=None,
+                   grad_out=None):
+    """The reference's math path (``python/densecore/functional.py:318-340``) composed from the
+    restated pieces: q and k each scaled by float32(sqrt(|scale|)), ``bmm``, the additive mask,
+    the safe softmax, an optional dropout noise tensor (keep / (1 - p) as float32), ``bmm`` with
+    v.  With ``grad_out`` it also returns (dq, dk, dv, dmask) by the chain rule of those ops
+    (``mm_mat1_backward`` / ``mm_mat2_backward``, ``softmax_backward_lastdim``, the masked
+    fills zeroing the empty rows)."""
+    import math
+    q, k, v = _f32(query), _f32(key), _f32(value)
+    E, L, S = q.shape[-1], q.shape[-2], k.shape[-2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(E) if E else 1.0
+    factor = math.sqrt(abs(scale))
+    fq = np.float32(-factor if scale < 0 else factor)
+    fk = np.float32(factor)
+    qs, ks = q * fq, k * fk
+    attn = bmm(qs, np.swapaxes(ks, -1, -2), b_k_contiguous=True)
+    mask = np.tril(np.ones((L, S), bool)) if is_causal else attn_mask
+    empty = None
+    if mask is not None:
+        mask = np.asarray(mask)
+        additive = np.where(mask, np.float32(0), np.float32(-np.inf)) if mask.dtype == np.bool_ \
+            else mask.astype(np.float32)
+        attn = attn + additive
+        empty = np.isneginf(attn).all(-1, keepdims=True)
+    if empty is not None and empty.any():
+        w = np.where(empty, np.float32(0), softmax(np.where(empty, np.float32(0), attn)))
+    else:
+        w = softmax(attn)
+    wd = w if noise is None else w * _f32(noise)
+    out = bmm(wd, v)
+    if grad_out is None:
+        return out
+    g = _f32(grad_out)
+    dwd = bmm(g, np.swapaxes(v, -1, -2))
+    dv = bmm(np.swapaxes(wd, -1, -2), g)
+    dw = dwd if noise is None else dwd * _f32(noise)
+    if empty is not None and empty.any():
+        dw = np.where(empty, np.float32(0), dw)
+        ws = softmax(np.where(empty, np.float32(0), attn))
+        da = np.where(empty, np.float32(0), softmax_backward(dw, ws))
+    else:
+        da = softmax_backward(dw, w)
+    dqs = bmm(da, ks)
+    dks = bmm(np.swapaxes(da, -1, -2), qs)
+    return out, (dqs * fq, dks * fk, dv, da)

@@ -18,6 +18,8 @@
  *   src/sleef.rs:1213-1255          exp_u20 (Arm Optimized Routines expf via PyTorch NEON),
  *                                   including its per-4-lane-group fallback to SLEEF expf
  *   src/torch_sum.rs:17-68          thread count (splits work only; never changes bits)
+ *   src/torch_softmax.rs:57-67,90-97  softmax_lastdim / softmax_backward_lastdim (the math
+ *                                   path's Tensor.softmax(-1) and its gradient)
  *
  * Build flags matter: -O2 -ffp-contract=off -fno-fast-math.  Rust never contracts a*b+c,
  * so every explicit Rust `mul_add` is an explicit fmaf here and nothing else is fused.
@@ -499,6 +501,44 @@ EXPORT int oracle_backward(const float *grad_out, const float *q, const float *k
     memset(gv, 0, batch * kv_heads * kv_len * head_dim * sizeof(float));
     par_tasks(batch * kv_heads, bwd_task, &c);
     return c.failed;
+}
+
+/* ---- torch_softmax.rs:14-37 reduce_all with op = add over plain values ---- */
+static float reduce_all_sum(const float *v, size_t size) {
+    if (size < 4) {
+        float acc = v[0];
+        for (size_t i = 1; i < size; ++i) acc = acc + v[i];
+        return acc;
+    }
+    float acc[4] = {v[0], v[1], v[2], v[3]};
+    size_t whole = size - size % 4, d = 4;
+    for (; d < whole; d += 4)
+        for (int l = 0; l < 4; ++l) acc[l] = acc[l] + v[d + l];
+    for (size_t l = 0; l < size - d; ++l) acc[l] = acc[l] + v[d + l];
+    return (acc[0] + acc[2]) + (acc[1] + acc[3]);
+}
+
+/* ---- torch_softmax.rs:57-67 softmax_lastdim: max, exp_array (SLEEF expf lane by lane,
+ * sleef.rs:1292-1298, 1502-1503), sum, then e * (1 / sum) ---- */
+EXPORT void oracle_softmax(const float *x, size_t rows, size_t width, float *y) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * width;
+        float *out = y + r * width;
+        const float max = reduce_all_max(row, width);
+        for (size_t i = 0; i < width; ++i) out[i] = sleef_expf(row[i] - max);
+        const float inv = 1.0f / reduce_all_sum(out, width);
+        for (size_t i = 0; i < width; ++i) out[i] = out[i] * inv;
+    }
+}
+
+/* ---- torch_softmax.rs:90-97 softmax_backward_lastdim: (g - sum(g * y)) * y ---- */
+EXPORT void oracle_softmax_backward(const float *g, const float *y, size_t rows, size_t width,
+                                    float *dx) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *gr = g + r * width, *yr = y + r * width;
+        const float sum = reduce_all_dot(gr, yr, width);
+        for (size_t i = 0; i < width; ++i) dx[r * width + i] = (gr[i] - sum) * yr[i];
+    }
 }
 
 /* ---- thread count, torch_sum.rs:51-68 ---- */

@@ -11,12 +11,16 @@ import pytest
 from densecore_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "dc_attn.h")
+INCLUDE = os.path.join(ROOT, "include")
 
 
 def header_functions():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(dc_[a-z_0-9]+)\s*\(", text)))
+    """Every function any header under include/ declares."""
+    names = set()
+    for h in sorted(os.listdir(INCLUDE)):
+        if h.endswith(".h"):
+            names |= set(re.findall(r"\b(dc_[a-z_0-9]+)\s*\(", open(os.path.join(INCLUDE, h)).read()))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
@@ -46,6 +50,51 @@ def test_descriptor_layout_matches_header(tmp_path):
     D = _lib.Desc
     assert got == [ctypes.sizeof(D), D.causal.offset, D.scale.offset, D.dtype.offset,
                    D.mask_stride_l.offset]
+
+
+def test_softmax_descriptor_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "dc_math.h"\n'
+                   "int main(void){printf(\"%zu %zu %zu %zu\\n\", sizeof(dc_softmax_desc),"
+                   " offsetof(dc_softmax_desc, q_len), offsetof(dc_softmax_desc, mask_stride_l),"
+                   " offsetof(dc_softmax_desc, safe));return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True,
+                                       check=True).stdout.split()))
+    D = _lib.SoftmaxDesc
+    assert got == [ctypes.sizeof(D), D.q_len.offset, D.mask_stride_l.offset, D.safe.offset]
+
+
+def softmax_desc(**kw):
+    d = dict(rows=6, width=5, heads=1, q_len=1, mask_stride_b=0, mask_stride_h=0,
+             mask_stride_l=0, safe=0, reserved=0)
+    d.update(kw)
+    return _lib.SoftmaxDesc(**d)
+
+
+@pytest.mark.parametrize("kw,use_mask,status,msg", [
+    (dict(width=0), False, _lib.DC_INVALID_ARGUMENT, "nonempty reduction axis"),
+    (dict(rows=0, width=0), False, _lib.DC_INVALID_ARGUMENT, "nonempty reduction axis"),
+    (dict(rows=-1), False, _lib.DC_INVALID_ARGUMENT, "negative"),
+    (dict(width=2**31), False, _lib.DC_UNSUPPORTED, "2\\^31"),
+    (dict(heads=4, q_len=4), True, _lib.DC_INVALID_ARGUMENT, "rows == B\\*H\\*L"),
+    (dict(heads=0), True, _lib.DC_INVALID_ARGUMENT, "rows == B\\*H\\*L"),
+    (dict(heads=2, q_len=3, mask_stride_l=-5), True, _lib.DC_INVALID_ARGUMENT, "non-negative"),
+    (dict(), False, _lib.DC_INVALID_ARGUMENT, "null pointer"),
+])
+def test_softmax_argument_errors(kw, use_mask, status, msg):
+    L = _lib.lib()
+    d = softmax_desc(**kw)
+    mask = ctypes.c_void_p(16) if use_mask else None   # never dereferenced: rejected first
+    assert L.dc_softmax_fwd(ctypes.byref(d), None, mask, None, None) == status
+    assert re.search(msg, L.dc_last_error().decode())
+
+
+def test_softmax_empty_rows_accepted():
+    L = _lib.lib()
+    assert L.dc_softmax_fwd(ctypes.byref(softmax_desc(rows=0)), None, None, None, None) == _lib.DC_OK
+    assert L.dc_softmax_bwd(ctypes.byref(softmax_desc(rows=0)), None, None, None, None) == _lib.DC_OK
 
 
 def desc(**kw):

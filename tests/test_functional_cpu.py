@@ -1,6 +1,7 @@
 """Host-side logic of the Python mirror, without a GPU: argument checks and messages follow
 python/densecore/functional.py:276-364 and src/lib.rs:555-683 of the reference; inputs the
-flash path does not take raise instead of falling back; masks become broadcast views."""
+flash path does not take go to the device math path and never run on the host; masks become
+broadcast views."""
 import numpy as np
 import pytest
 
@@ -31,19 +32,23 @@ def test_reference_argument_errors():
         sdpa(np.zeros((1, 1, 2, 4)), k, k)
 
 
-def test_math_path_inputs_are_refused_not_emulated():
+def test_math_path_inputs_never_run_on_the_cpu():
+    """Inputs the flash path does not take go to the composed math path, which runs on the GPU
+    only: CPU tensors are rejected rather than computed on the host."""
     sdpa = F.scaled_dot_product_attention
     q, k = t(1, 1, 2, 4), t(1, 1, 3, 4)
-    with pytest.raises(NotImplementedError, match="math path"):
-        sdpa(q, k, k, dropout_p=0.5)
-    with pytest.raises(NotImplementedError, match="math path"):
-        sdpa(t(1, 2, 4), t(1, 3, 4), t(1, 3, 4))  # rank 3
-    with pytest.raises(NotImplementedError, match="math path"):
-        sdpa(q, k, t(1, 1, 3, 5))  # Ev != E
-    with pytest.raises(NotImplementedError, match="math path"):
-        sdpa(q, k, k, attn_mask=np.zeros((1, 2, 3), np.float32))  # 3-D mask
-    with pytest.raises(NotImplementedError, match="math path"):
+    for call in (lambda: sdpa(q, k, k, dropout_p=0.5),
+                 lambda: sdpa(t(1, 2, 4), t(1, 3, 4), t(1, 3, 4)),          # rank 3
+                 lambda: sdpa(q, k, t(1, 1, 3, 5)),                          # Ev != E
+                 lambda: sdpa(q, k, k, attn_mask=np.zeros((1, 2, 3), np.float32))):  # 3-D mask
+        with pytest.raises(ValueError, match="GPU"):
+            call()
+    with pytest.raises(NotImplementedError, match="float32"):
         sdpa(q.double(), k.double(), k.double())
+    with pytest.raises(ValueError, match="GPU"):
+        _native._softmax(t(2, 3))
+    with pytest.raises(ValueError, match="GPU"):
+        F.softmax(t(2, 3))
 
 
 def test_cpu_tensors_are_rejected_no_fallback():
