@@ -17,7 +17,10 @@ EXPORTS = ("dc_abi_version", "dc_last_error",
            "dc_sdpa_fwd_workspace_size", "dc_sdpa_fwd",
            "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
            "dc_sdpa_decode_workspace_size", "dc_sdpa_decode",
-           "dc_softmax_fwd", "dc_softmax_bwd")
+           "dc_softmax_fwd", "dc_softmax_bwd",
+           "dc_mt19937_seed", "dc_mt19937_advance", "dc_mt19937_table_bytes",
+           "dc_mt19937_table_init", "dc_bernoulli_max_draws", "dc_bernoulli_workspace_size",
+           "dc_bernoulli", "dc_dropout_apply")
 
 
 class Desc(ctypes.Structure):
@@ -62,8 +65,22 @@ def lib():
         SD = ctypes.POINTER(SoftmaxDesc)
         L.dc_softmax_fwd.argtypes = [SD, P, P, P, P]
         L.dc_softmax_bwd.argtypes = [SD, P, P, P, P]
+        I64P = ctypes.POINTER(ctypes.c_int64)
+        L.dc_mt19937_seed.argtypes = [ctypes.c_uint64, P]
+        L.dc_mt19937_seed.restype = None
+        L.dc_mt19937_advance.argtypes = [P, I64P, I64P, ctypes.c_uint64]
+        L.dc_mt19937_table_bytes.argtypes = []
+        L.dc_mt19937_table_bytes.restype = SZ
+        L.dc_mt19937_table_init.argtypes = [P, P]
+        L.dc_bernoulli_max_draws.argtypes = []
+        L.dc_bernoulli_max_draws.restype = ctypes.c_int64
+        L.dc_bernoulli_workspace_size.argtypes = [ctypes.c_int64]
+        L.dc_bernoulli_workspace_size.restype = SZ
+        L.dc_bernoulli.argtypes = [P, P, I64P, I64P, ctypes.c_int64, ctypes.c_double, P, P, SZ, P]
+        L.dc_dropout_apply.argtypes = [P, ctypes.c_int64, ctypes.c_float, P, P, P]
         for name in ("dc_sdpa_fwd", "dc_sdpa_bwd", "dc_sdpa_decode", "dc_softmax_fwd",
-                     "dc_softmax_bwd"):
+                     "dc_softmax_bwd", "dc_mt19937_advance", "dc_mt19937_table_init",
+                     "dc_bernoulli", "dc_dropout_apply"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib

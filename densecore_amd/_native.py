@@ -195,6 +195,20 @@ def _softmax_backward(grad_y, y):
     return dx
 
 
+def _dropout_apply(bits, x, scale):
+    """``x * noise`` for the keep bits of ``x``'s elements in row-major order:
+    y = x * (kept ? scale : 0) (``dc_dropout_apply``)."""
+    if x.device.type != "cuda" or x.dtype != torch.float32 or bits.device != x.device:
+        raise ValueError("dropout takes float32 tensors and keep bits on one GPU")
+    x = x.contiguous()
+    if bits.numel() * 32 < x.numel():
+        raise ValueError("dropout keep bits do not cover the tensor")
+    y = torch.empty_like(x)
+    _lib.check(_lib.lib().dc_dropout_apply(_ptr(bits), x.numel(), float(scale), _ptr(x), _ptr(y),
+                                           _stream(x.device)))
+    return y
+
+
 def default_scale(head_dim):
     """``sdp::calculate_scale`` as the Python layer passes it (a double)."""
     return 1.0 / math.sqrt(head_dim) if head_dim else 1.0

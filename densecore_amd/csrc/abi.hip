@@ -135,6 +135,28 @@ bool softmax_vec(const dc::SoftmaxArgs &a, const void *p0, const void *p1, const
     return v;
 }
 
+// The reference's engine position (src/torch_random.rs:79-91, from_words :290-296): the next
+// output's index relative to the current block, r in [0, 624].
+dc_status mt_position(const void *words, const int64_t *left, const int64_t *next, int64_t *r) {
+    if (words == nullptr || left == nullptr || next == nullptr)
+        return fail(DC_INVALID_ARGUMENT, "invalid generator state");
+    const int64_t l = *left, n = *next;
+    if (l < 1 || l > dc::mt::kState || n < 0 || n > dc::mt::kState)
+        return fail(DC_INVALID_ARGUMENT, "invalid generator state");
+    if (l == 1) {
+        *r = dc::mt::kState;
+        return ok();
+    }
+    if (l + n != dc::mt::kState + 1) return fail(DC_INVALID_ARGUMENT, "invalid generator state");
+    *r = n;
+    return ok();
+}
+
+int bernoulli_chunks(int64_t n) {
+    if (n <= dc::mt::kHead) return 0;
+    return (int)((n - dc::mt::kHead + dc::mt::kChunkWords / 2 - 1) / (dc::mt::kChunkWords / 2));
+}
+
 }  // namespace
 
 extern "C" {
@@ -265,6 +287,100 @@ dc_status dc_softmax_bwd(const dc_softmax_desc *d, const float *grad_y, const fl
     a.out = grad_x;
     return launched(dc::launch_softmax_bwd(a, softmax_vec(a, grad_y, y, grad_x),
                                            static_cast<hipStream_t>(stream)));
+}
+
+void dc_mt19937_seed(uint64_t seed, uint32_t *words) {
+    if (words == nullptr) return;
+    words[0] = (uint32_t)seed;
+    for (int j = 1; j < dc::mt::kState; ++j)
+        words[j] = 1812433253u * (words[j - 1] ^ (words[j - 1] >> 30)) + (uint32_t)j;
+}
+
+dc_status dc_mt19937_advance(uint32_t *words, int64_t *left, int64_t *next, uint64_t count) {
+    int64_t r;
+    dc_status st = mt_position(words, left, next, &r);
+    if (st != DC_OK) return st;
+    if (count == 0) return ok();
+    if (!dc::mt::tables_ready())
+        return fail(DC_EXECUTION_FAILED, "mt19937 jump-ahead tables could not be built");
+    const uint64_t last = (uint64_t)r + count - 1;
+    const uint64_t block = last / dc::mt::kState;
+    if (block > 0) {
+        uint32_t w1[dc::mt::kState];
+        dc::mt::twist_block_host(words, w1);
+        dc::mt::jump_window_host(w1, (block - 1) * dc::mt::kState, words);
+    }
+    *next = (int64_t)(last - block * dc::mt::kState) + 1;
+    *left = dc::mt::kState + 1 - *next;
+    return ok();
+}
+
+size_t dc_mt19937_table_bytes(void) {
+    return (size_t)dc::mt::kTablePolys * dc::mt::kTableWords * sizeof(uint32_t);
+}
+
+dc_status dc_mt19937_table_init(void *table, void *stream) {
+    if (table == nullptr) return fail(DC_INVALID_ARGUMENT, "mt19937 table pointer is null");
+    const uint32_t *w = dc::mt::table_words();
+    if (w == nullptr) return fail(DC_EXECUTION_FAILED, "mt19937 jump-ahead tables could not be built");
+    const hipError_t e = hipMemcpyAsync(table, w, dc_mt19937_table_bytes(), hipMemcpyHostToDevice,
+                                        static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return fail(DC_EXECUTION_FAILED, std::string("HIP copy failed: ") + hipGetErrorString(e));
+    return ok();
+}
+
+int64_t dc_bernoulli_max_draws(void) {
+    return dc::mt::kHead + (int64_t)dc::mt::kMaxChunks * (dc::mt::kChunkWords / 2);
+}
+
+size_t dc_bernoulli_workspace_size(int64_t n) {
+    if (n < 0 || n > dc_bernoulli_max_draws()) return 0;
+    return round_up(dc::mt::window_words(bernoulli_chunks(n)) * sizeof(uint32_t));
+}
+
+dc_status dc_bernoulli(const void *table, uint32_t *state, int64_t *left, int64_t *next,
+                       int64_t n, double p, uint32_t *keep_bits, void *workspace,
+                       size_t workspace_bytes, void *stream) {
+    int64_t r;
+    dc_status st = mt_position(state, left, next, &r);
+    if (st != DC_OK) return st;
+    if (n < 0) return fail(DC_INVALID_ARGUMENT, "bernoulli count is negative");
+    if (!(p >= 0.0 && p <= 1.0)) return fail(DC_INVALID_ARGUMENT, "bernoulli expects 0 <= p <= 1");
+    if (n > dc_bernoulli_max_draws())
+        return fail(DC_UNSUPPORTED, "bernoulli draws more than dc_bernoulli_max_draws() in one call");
+    if (n == 0) return ok();
+    if (table == nullptr || keep_bits == nullptr || workspace == nullptr)
+        return fail(DC_INVALID_ARGUMENT, "bernoulli got a null pointer");
+    if (workspace_bytes < dc_bernoulli_workspace_size(n))
+        return fail(DC_INVALID_ARGUMENT, "bernoulli workspace is too small");
+    dc::mt::MtArgs a{};
+    a.state = state;
+    a.bits = keep_bits;
+    a.win = static_cast<uint32_t *>(workspace);
+    a.n = n;
+    a.p = p;
+    a.r = (int)r;
+    a.eh = dc::mt::kHead;
+    a.a0 = a.r + 2 * a.eh;
+    const int64_t last = r + 2 * n - 1;
+    a.state_block = last / dc::mt::kState;
+    st = launched(dc::mt::launch_bernoulli(a, static_cast<const uint32_t *>(table), bernoulli_chunks(n),
+                                           a.win, static_cast<hipStream_t>(stream)));
+    if (st != DC_OK) return st;
+    *next = last - a.state_block * dc::mt::kState + 1;
+    *left = dc::mt::kState + 1 - *next;
+    return ok();
+}
+
+dc_status dc_dropout_apply(const uint32_t *keep_bits, int64_t n, float scale, const float *x,
+                           float *y, void *stream) {
+    if (n < 0) return fail(DC_INVALID_ARGUMENT, "dropout count is negative");
+    if (n == 0) return ok();
+    if (keep_bits == nullptr || x == nullptr || y == nullptr)
+        return fail(DC_INVALID_ARGUMENT, "dropout got a null pointer");
+    if (n > (int64_t)256 * INT32_MAX) return fail(DC_UNSUPPORTED, "dropout count exceeds 2^39");
+    return launched(dc::mt::launch_dropout_apply(keep_bits, n, scale, x, y, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -1,0 +1,421 @@
+// The reference's CPU generator stream (src/torch_random.rs:9-98, PyTorch's mt19937) drawn on
+// the GPU, for dropout masks that are bit-identical to Generator::bernoulli
+// (src/torch_random.rs:241-254): element e keeps iff the double built from outputs 2e and
+// 2e + 1, (hi << 32 | lo) & (2^53 - 1) times 2^-53, is below p.
+//
+// The engine's untempered words satisfy x[t + 624] = x[t + 397] ^ twist(x[t], x[t + 1]) for every
+// t >= 0 (the in-place update of next_state, src/torch_random.rs:66-77), so the stream is one
+// linear recurrence over GF(2).  A window of 624 consecutive words that follows at least one
+// update lies in the 19937-dimensional subspace on which that recurrence has the primitive
+// characteristic polynomial phi (degree 19937), so the window d words later is
+//     W(t + d) = sum_i g_i W(t + i),   g = z^d mod phi,
+// a XOR of shifted copies of the sequence (the standard jump-ahead of F2-linear generators).
+//
+// Layout of one draw of n elements (positions relative to the start of the engine's current
+// block of 624 words, r = position of the next output):
+//   head      elements [0, Eh), Eh = 64: generated from the current block by one workgroup
+//             (mt_base_kernel), which also writes the window at A0 = r + 2 Eh (A0 >= 1, so that
+//             window follows an update even when the block is a freshly seeded one);
+//   chunks    chunk c covers elements [Eh + c J/2, Eh + (c + 1) J/2), J = 2^17 words; its window
+//             is W(A0 + c J), reached from W(A0) through a radix-16 tree of jumps (c = 256 c3 +
+//             16 c2 + c1: jumps by c3 2^25, then c2 2^21, then c1 2^17; mt_jump_kernel), and
+//             one wave generates its words from that window (mt_chunk_kernel).
+// Keep bits: element e is bit e % 32 of word e / 32 (heads and chunks write whole words).  The
+// engine block that holds the last output drawn is written back to the state (by the base
+// workgroup or by the chunk whose range holds the block's first word), and the host moves
+// (left, next) the way next_state/random do.
+//
+// The jump polynomials (48 of them) are computed once on the host: phi by Berlekamp-Massey on
+// 2 * 19937 bits of the stream, then z^(digit * 2^(17 + 4 level)) mod phi by squaring and
+// multiplying; the caller uploads them into its own device buffer (dc_mt19937_table_init).
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+#include "params.hpp"
+
+namespace dc {
+namespace mt {
+
+namespace {
+
+// ---------------------------------------------------------------- host: GF(2) polynomials
+
+constexpr int kPW = kTableWords / 2;  // 312 uint64 words: 19968 bits, degree < 19937 fits
+
+inline uint32_t twist(uint32_t u, uint32_t v) {
+    return (((u & 0x80000000u) | (v & 0x7fffffffu)) >> 1) ^ ((v & 1u) ? 0x9908b0dfu : 0u);
+}
+
+typedef std::vector<uint64_t> Bits;  // bit i of a polynomial = coefficient of z^i
+
+inline bool bit(const Bits &a, int i) { return (a[i >> 6] >> (i & 63)) & 1u; }
+inline void flip(Bits &a, int i) { a[i >> 6] ^= 1ull << (i & 63); }
+
+// a ^= b << s (b has nb words; a is large enough).
+void xor_shifted(Bits &a, const Bits &b, int nb, int s) {
+    const int ws = s >> 6, bs = s & 63;
+    for (int i = 0; i < nb; ++i) {
+        if (!b[i]) continue;
+        a[i + ws] ^= b[i] << bs;
+        if (bs) a[i + ws + 1] ^= b[i] >> (64 - bs);
+    }
+}
+
+// Characteristic polynomial of the engine: Berlekamp-Massey on bit 0 of the untempered words
+// x[624 .. 624 + 2 * 19937) of the engine seeded with 5489.
+Bits char_poly() {
+    const int n = 2 * kDegree;
+    std::vector<uint32_t> x(kState + n + 1);
+    x[0] = 5489u;
+    for (int j = 1; j < kState; ++j) x[j] = 1812433253u * (x[j - 1] ^ (x[j - 1] >> 30)) + (uint32_t)j;
+    for (int t = 0; t + kState < (int)x.size(); ++t)
+        x[t + kState] = x[t + kM] ^ twist(x[t], x[t + 1]);
+    const int W = kPW + 1;
+    Bits C(W + 1, 0), B(W + 1, 0), R(W + 1, 0), T;
+    C[0] = B[0] = 1;
+    int L = 0, m = 1;
+    for (int k = 0; k < n; ++k) {
+        // R bit j = s[k - j]: shift in s[k].
+        for (int w = W; w > 0; --w) R[w] = (R[w] << 1) | (R[w - 1] >> 63);
+        R[0] = (R[0] << 1) | (x[kState + k] & 1u);
+        int d = 0;
+        for (int w = 0; w <= W; ++w) d ^= __builtin_popcountll(C[w] & R[w]) & 1;
+        if (!d) {
+            ++m;
+        } else if (2 * L <= k) {
+            T = C;
+            xor_shifted(C, B, W + 1 - (m >> 6) - 1, m);
+            L = k + 1 - L;
+            B = T;
+            m = 1;
+        } else {
+            xor_shifted(C, B, W + 1 - (m >> 6) - 1, m);
+            ++m;
+        }
+    }
+    // phi(z) = z^L C(1/z).
+    Bits phi(kPW, 0);
+    if (L != kDegree) return Bits();
+    for (int i = 0; i <= L; ++i)
+        if (bit(C, i)) flip(phi, L - i);
+    return phi;
+}
+
+struct Field {
+    Bits phi;
+
+    // a * b mod phi, both of degree < 19937.
+    Bits mul(const Bits &a, const Bits &b) const {
+        Bits tab[16];
+        for (int w = 0; w < 16; ++w) {
+            tab[w].assign(kPW + 1, 0);
+            for (int s = 0; s < 4; ++s)
+                if (w >> s & 1) xor_shifted(tab[w], b, kPW, s);
+        }
+        Bits r(2 * kPW + 2, 0);
+        for (int p = 0; p < kPW * 16; ++p) {
+            const int nib = (int)(a[p >> 4] >> (4 * (p & 15))) & 15;
+            if (nib) xor_shifted(r, tab[nib], kPW + 1, 4 * p);
+        }
+        return reduce(r);
+    }
+
+    // r mod phi for any length of r (top-down: each step clears bit i and touches no bit above).
+    Bits reduce(Bits r) const {
+        const int top = (int)r.size() * 64 - 1;
+        r.resize(r.size() + kPW + 2, 0);
+        for (int i = top; i >= kDegree; --i)
+            if (bit(r, i)) xor_shifted(r, phi, kPW, i - kDegree);
+        r.resize(kPW);
+        return r;
+    }
+
+    // z^e mod phi (square and multiply from the top set bit of e).
+    Bits pow_z(uint64_t e) const {
+        Bits r(kPW, 0);
+        r[0] = 1;
+        for (int b = 63 - (e ? __builtin_clzll(e) : 63); b >= 0; --b) {
+            r = mul(r, r);
+            if (e >> b & 1) {
+                Bits s(kPW + 1, 0);
+                xor_shifted(s, r, kPW, 1);
+                r = reduce(s);
+            }
+        }
+        return r;
+    }
+};
+
+struct Tables {
+    bool ok = false;
+    Field f;
+    std::vector<uint32_t> words;  // kTablePolys polynomials of kTableWords uint32 words
+};
+
+const Tables &tables() {
+    static Tables t;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        t.f.phi = char_poly();
+        if (t.f.phi.empty()) return;
+        t.words.assign((size_t)kTablePolys * kTableWords, 0);
+        Bits base = t.f.pow_z(1ull << kChunkLog2);  // z^(2^17)
+        for (int level = 0; level < kJumpLevels; ++level) {
+            Bits p(kPW, 0);
+            p[0] = 1;
+            for (int digit = 0; digit < kRadix; ++digit) {
+                uint32_t *dst = &t.words[((size_t)level * kRadix + digit) * kTableWords];
+                std::memcpy(dst, p.data(), kTableWords * sizeof(uint32_t));
+                p = t.f.mul(p, base);
+            }
+            base = p;  // base^16
+        }
+        t.ok = true;
+    });
+    return t;
+}
+
+// The window d words after `win` (which must follow at least one engine update).
+void jump_host(const Field &f, const uint32_t *win, uint64_t d, uint32_t *out) {
+    const Bits g = f.pow_z(d);
+    std::vector<uint32_t> seq(kState + kDegree + 1);
+    std::memcpy(seq.data(), win, kState * sizeof(uint32_t));
+    for (int t = 0; t + kState < (int)seq.size(); ++t)
+        seq[t + kState] = seq[t + kM] ^ twist(seq[t], seq[t + 1]);
+    std::vector<uint32_t> acc(kState, 0);
+    for (int i = 0; i < kDegree; ++i)
+        if (bit(g, i))
+            for (int j = 0; j < kState; ++j) acc[j] ^= seq[i + j];
+    std::memcpy(out, acc.data(), kState * sizeof(uint32_t));
+}
+
+// ---------------------------------------------------------------- device
+
+DEVI uint32_t twist_d(uint32_t u, uint32_t v) {
+    return (((u & 0x80000000u) | (v & 0x7fffffffu)) >> 1) ^ ((v & 1u) ? 0x9908b0dfu : 0u);
+}
+
+// src/torch_random.rs:86-89.
+DEVI uint32_t temper(uint32_t y) {
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+// uniform_f64 (src/torch_random.rs:106-110) of the pair (hi, lo) compared with p: the product
+// is exact, and mul_add(1, 0) leaves it unchanged.
+DEVI bool keep(uint32_t hi, uint32_t lo, double p) {
+    const uint64_t r = (((uint64_t)hi << 32) | lo) & ((1ull << 53) - 1);
+    return (double)r * 0x1p-53 < p;
+}
+
+// One workgroup: the current block `state` (positions 0..623), the words after it up to
+// A0 + 623, the head's keep bits, the window at A0, and (when the last drawn output lies before
+// A0) the engine block that holds it.
+constexpr int kBaseWords = 2048;
+
+__global__ __launch_bounds__(256) void mt_base_kernel(MtArgs a) {
+    __shared__ uint32_t x[kBaseWords];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kState; i += 256) x[i] = a.state[i];
+    __syncthreads();
+    const int total = a.a0 + kState;  // positions [0, total) are needed
+    for (int base = kState; base < total; base += 128) {
+        const int u = base + tid;
+        if (tid < 128 && u < total) x[u] = x[u - 227] ^ twist_d(x[u - 624], x[u - 623]);
+        __syncthreads();
+    }
+    // Head elements [0, min(Eh, n)): outputs r + 2e, r + 2e + 1, 64 elements per wave pass.
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t head = a.n < a.eh ? a.n : a.eh;
+    for (int e0 = wave * 64; e0 < a.eh; e0 += 256) {
+        const int e = e0 + lane;
+        bool k = false;
+        if (e < head) k = keep(temper(x[a.r + 2 * e]), temper(x[a.r + 2 * e + 1]), a.p);
+        const uint64_t m = __ballot(k);
+        if (e0 < head) {
+            if (lane == 0) a.bits[e0 >> 5] = (uint32_t)m;
+            if (lane == 1 && e0 + 32 < head) a.bits[(e0 >> 5) + 1] = (uint32_t)(m >> 32);
+        }
+    }
+    for (int i = tid; i < kState; i += 256) a.win[i] = x[a.a0 + i];
+    if (a.state_block >= 0 && a.state_block * kState < a.a0)
+        for (int i = tid; i < kState; i += 256) a.state[i] = x[a.state_block * kState + i];
+}
+
+// One workgroup per destination window: dst[w] = W(src[w / 16] + digit * step), digit = w % 16,
+// with g = table[level][digit].  Threads t < 78 own output words 8t .. 8t + 7 and slide an
+// 8-word register window along the sequence, which is generated into an LDS ring 1024 words
+// ahead of the sum.
+constexpr int kRing = 2048;
+constexpr int kSeg = 1024;
+
+__global__ __launch_bounds__(128) void mt_jump_kernel(const uint32_t *src, uint32_t *dst,
+                                                      const uint32_t *table, int level, int count) {
+    __shared__ uint32_t ring[kRing];
+    const int w = blockIdx.x;
+    if (w >= count) return;
+    const int digit = w % kRadix;
+    const uint32_t *in = src + (size_t)(w / kRadix) * kState;
+    uint32_t *out = dst + (size_t)w * kState;
+    const int tid = threadIdx.x;
+    if (digit == 0) {
+        for (int i = tid; i < kState; i += 128) out[i] = in[i];
+        return;
+    }
+    const uint32_t *g = table + ((size_t)level * kRadix + digit) * kTableWords;
+    for (int i = tid; i < kState; i += 128) ring[i] = in[i];
+    int made = kState;
+    uint32_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool owner = tid < kState / 8;
+    for (int seg = 0; seg < kDegree; seg += kSeg) {
+        const int seg_end = seg + kSeg < kDegree + 7 ? seg + kSeg : kDegree + 7;  // i < seg_end
+        const int need = (seg_end + 7) / 8 * 8 + kState + 8;  // words read by this segment
+        __syncthreads();
+        while (made < need) {
+            const int u = made + tid;
+            if (u < need)
+                ring[u & (kRing - 1)] = ring[(u - 227) & (kRing - 1)] ^
+                                        twist_d(ring[(u - 624) & (kRing - 1)], ring[(u - 623) & (kRing - 1)]);
+            made = made + 128 < need ? made + 128 : need;  // the next segment continues at `need`
+            __syncthreads();
+        }
+        if (owner) {
+            const int j0 = 8 * tid;
+            uint32_t cur[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cur[u] = ring[(seg + j0 + u) & (kRing - 1)];
+            for (int i0 = seg; i0 < seg_end; i0 += 8) {
+                uint32_t nxt[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) nxt[u] = ring[(i0 + 8 + j0 + u) & (kRing - 1)];
+                const uint32_t gb = (g[i0 >> 5] >> (i0 & 31)) & 0xffu;  // g bits i0 .. i0 + 7
+                if (gb) {
+#pragma unroll
+                    for (int d = 0; d < 8; ++d) {
+                        if (gb >> d & 1u) {
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) acc[u] ^= (d + u < 8) ? cur[d + u] : nxt[d + u - 8];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+            }
+        }
+    }
+    if (owner)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) out[8 * tid + u] = acc[u];
+}
+
+// One wave per chunk: words A0 + c J .. from its window, 64 elements (128 words) per step.
+__global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *wins) {
+    __shared__ uint32_t ring[1024];
+    const int c = blockIdx.x;
+    const int lane = threadIdx.x;
+    const uint32_t *win = wins + (size_t)c * kState;
+    for (int i = lane; i < kState; i += 64) ring[i] = win[i];
+    const int64_t e_begin = a.eh + (int64_t)c * (kChunkWords / 2);
+    int64_t e_end = e_begin + kChunkWords / 2;
+    if (e_end > a.n) e_end = a.n;
+    // The engine block holding the last output: does it start inside this chunk's words?
+    const int64_t chunk_pos = a.a0 + (int64_t)c * kChunkWords;  // relative position of word 0
+    const int64_t sb = a.state_block >= 0 ? (int64_t)a.state_block * kState - chunk_pos : -1;
+    const bool writes_state = a.state_block >= 0 && a.state_block * (int64_t)kState >= a.a0 &&
+                              sb >= 0 && sb < kChunkWords;
+    const int64_t words = writes_state && sb + kState > 2 * (e_end - e_begin)
+                              ? sb + kState : 2 * (e_end - e_begin);
+    __syncthreads();
+    for (int64_t base = 0; base < words; base += 128) {
+        const int u0 = (int)base + 2 * lane;
+        uint32_t w0, w1;
+        if (u0 < kState) {
+            w0 = ring[u0];
+            w1 = ring[u0 + 1];
+        } else {
+            w0 = ring[(u0 - 227) & 1023] ^ twist_d(ring[(u0 - 624) & 1023], ring[(u0 - 623) & 1023]);
+            w1 = ring[(u0 - 226) & 1023] ^ twist_d(ring[(u0 - 623) & 1023], ring[(u0 - 622) & 1023]);
+            ring[u0 & 1023] = w0;
+            ring[(u0 + 1) & 1023] = w1;
+        }
+        const int64_t e = e_begin + base / 2 + lane;
+        const bool k = e < e_end && keep(temper(w0), temper(w1), a.p);
+        const uint64_t m = __ballot(k);
+        const int64_t e0 = e_begin + base / 2;
+        if (e0 < e_end) {
+            if (lane == 0) a.bits[e0 >> 5] = (uint32_t)m;
+            if (lane == 1 && e0 + 32 < e_end) a.bits[(e0 >> 5) + 1] = (uint32_t)(m >> 32);
+        }
+        __syncthreads();
+        if (writes_state && base + 128 >= sb + kState && base < sb + kState) {
+            // Words sb .. sb + 623 are the last <= 752 words made: all still in the ring.
+            for (int i = lane; i < kState; i += 64) a.state[i] = ring[(sb + i) & 1023];
+        }
+    }
+}
+
+// y = x * (keep ? scale : 0): the reference's input * noise, noise = bernoulli / float32(1 - p)
+// (python/densecore/functional.py:244, 638-641).
+__global__ __launch_bounds__(256) void dropout_apply_kernel(const uint32_t *bits, int64_t n, float scale,
+                                                            const float *x, float *y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const bool k = (bits[i >> 5] >> (i & 31)) & 1u;
+    y[i] = x[i] * (k ? scale : 0.0f);
+}
+
+}  // namespace
+
+size_t window_words(int chunks) {
+    if (chunks == 0) return kState;
+    const int n3 = (chunks + kRadix * kRadix - 1) / (kRadix * kRadix);
+    const int n2 = (chunks + kRadix - 1) / kRadix;
+    return (size_t)(1 + n3 + n2 + chunks) * kState;
+}
+
+bool tables_ready() { return tables().ok; }
+
+const uint32_t *table_words() { return tables().ok ? tables().words.data() : nullptr; }
+
+bool jump_window_host(const uint32_t *win, uint64_t d, uint32_t *out) {
+    const Tables &t = tables();
+    if (!t.ok) return false;
+    jump_host(t.f, win, d, out);
+    return true;
+}
+
+void twist_block_host(const uint32_t *in, uint32_t *out) {
+    uint32_t x[2 * kState];
+    std::memcpy(x, in, kState * sizeof(uint32_t));
+    for (int t = 0; t < kState; ++t) x[t + kState] = x[t + kM] ^ twist(x[t], x[t + 1]);
+    std::memcpy(out, x + kState, kState * sizeof(uint32_t));
+}
+
+hipError_t launch_bernoulli(const MtArgs &a, const uint32_t *table, int chunks, uint32_t *wins,
+                            hipStream_t st) {
+    return_if(launch(mt_base_kernel, dim3(1), dim3(256), st, a));
+    if (chunks == 0) return hipSuccess;
+    // Radix-16 tree: level 2 (c3), level 1 (c2), level 0 (c1).  Window arrays are carved from
+    // `wins` (window_words(chunks) words): [W(A0)] [n3 level-2] [n2 level-1] [chunks].
+    const int n3 = (chunks + kRadix * kRadix - 1) / (kRadix * kRadix);
+    const int n2 = (chunks + kRadix - 1) / kRadix;
+    uint32_t *l3 = wins + kState, *l2 = l3 + (size_t)n3 * kState, *l1 = l2 + (size_t)n2 * kState;
+    return_if(launch(mt_jump_kernel, dim3(n3), dim3(128), st, (const uint32_t *)wins, l3, table, 2, n3));
+    return_if(launch(mt_jump_kernel, dim3(n2), dim3(128), st, (const uint32_t *)l3, l2, table, 1, n2));
+    return_if(launch(mt_jump_kernel, dim3(chunks), dim3(128), st, (const uint32_t *)l2, l1, table, 0, chunks));
+    return launch(mt_chunk_kernel, dim3(chunks), dim3(64), st, a, (const uint32_t *)l1);
+}
+
+hipError_t launch_dropout_apply(const uint32_t *bits, int64_t n, float scale, const float *x, float *y,
+                                hipStream_t st) {
+    const int64_t blocks = (n + 255) / 256;
+    return launch(dropout_apply_kernel, dim3((unsigned)blocks), dim3(256), st, bits, n, scale, x, y);
+}
+
+}  // namespace mt
+}  // namespace dc

@@ -66,6 +66,36 @@ int decode_splits(const AttnShape &s, int *split_len);
 hipError_t launch_softmax_fwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
 hipError_t launch_softmax_bwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
 
+// The reference's generator stream on the GPU (mt19937.hip).
+namespace mt {
+constexpr int kState = 624, kM = 397, kDegree = 19937;
+constexpr int kTableWords = 624;  // uint32 words per jump polynomial (19968 bits)
+constexpr int kRadix = 16, kJumpLevels = 3, kTablePolys = kRadix * kJumpLevels;
+constexpr int kChunkLog2 = 17, kChunkWords = 1 << kChunkLog2;  // words per chunk (one wave)
+constexpr int kHead = 64;                                       // elements of the base workgroup
+constexpr int kMaxChunks = kRadix * kRadix * kRadix;
+
+struct MtArgs {
+    uint32_t *state;      // the engine block (624 words), in/out
+    uint32_t *bits;       // keep bits, element e = bit e % 32 of word e / 32
+    uint32_t *win;        // out: the window at A0
+    int64_t n;            // elements
+    double p;             // keep iff uniform double < p
+    int r, a0, eh;        // first output, first chunk word (relative to the block), head elements
+    int64_t state_block;  // block (relative) holding the last output, or -1 when n == 0
+};
+
+size_t window_words(int chunks);
+bool tables_ready();
+const uint32_t *table_words();
+bool jump_window_host(const uint32_t *win, uint64_t d, uint32_t *out);
+void twist_block_host(const uint32_t *in, uint32_t *out);
+hipError_t launch_bernoulli(const MtArgs &a, const uint32_t *table, int chunks, uint32_t *wins,
+                            hipStream_t st);
+hipError_t launch_dropout_apply(const uint32_t *bits, int64_t n, float scale, const float *x,
+                                float *y, hipStream_t st);
+}  // namespace mt
+
 // Largest head dim each kernel family instantiates.
 constexpr int kMaxHeadDim = 256;
 

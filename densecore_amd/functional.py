@@ -147,9 +147,56 @@ def softmax(input, dim=-1):
     return _Softmax.apply(input, None, False)
 
 
+def _dropout_probability(p):
+    """``python/densecore/functional.py:219-226``."""
+    if isinstance(p, (bool, np.bool_)) or not isinstance(p, numbers.Real):
+        raise TypeError("dropout probability must be real")
+    p = float(p)
+    if not 0.0 <= p <= 1.0:
+        raise ValueError("dropout probability must be in [0, 1]")
+    return p
+
+
+class _Dropout(torch.autograd.Function):
+    """``input * noise`` with noise = keep / float32(1 - p): the same product forward and
+    backward (``dc_dropout_apply``)."""
+
+    @staticmethod
+    def forward(ctx, x, bits, scale):
+        ctx.save_for_backward(bits)
+        ctx.scale = scale
+        return _native._dropout_apply(bits, x, scale)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (bits,) = ctx.saved_tensors
+        return _native._dropout_apply(bits, grad, ctx.scale), None, None
+
+
 def dropout(input, p=0.5, training=True, generator=None):
-    """``functional.dropout`` (``python/densecore/functional.py:229-244``)."""
-    raise NotImplementedError("dropout on the GPU is not built yet")
+    """``functional.dropout`` (``python/densecore/functional.py:229-244``): zero elements with
+    probability p and scale survivors by 1/(1-p) while training.  The mask is
+    ``Generator::bernoulli(n, 1 - p)`` drawn on the GPU from the reference's generator stream
+    (``densecore_amd.random``), so a seed gives the reference's mask bit for bit; the noise
+    value is float32(1) / float32(1 - p) as ``_dropout_noise`` (:638-641) rounds it."""
+    from . import random as _random
+    if not isinstance(input, torch.Tensor):
+        raise TypeError("dropout input must be a Tensor")
+    p = _dropout_probability(p)
+    if type(training) is not bool:
+        raise TypeError("training must be a bool")
+    if not training or p == 0.0:
+        return input
+    if p == 1.0:
+        return input * torch.zeros((), dtype=input.dtype, device=input.device)
+    if input.device.type != "cuda":
+        raise ValueError("dropout on this path takes tensors on the GPU")
+    if input.dtype != torch.float32:
+        raise NotImplementedError("dropout on the GPU takes float32 tensors")
+    gen = _random.default_generator(input.device) if generator is None else generator
+    bits = gen._bernoulli_bits(input.numel(), 1 - p)
+    scale = float(np.float32(1.0) / np.float32(1 - p))
+    return _Dropout.apply(input, bits, scale)
 
 
 def _flash_mask(attn_mask, qshape, source, device):

@@ -65,6 +65,13 @@ def lib():
         L.oracle_scale_factor.restype = ctypes.c_float
         L.oracle_q_split.argtypes = [_SZ]
         L.oracle_q_split.restype = _SZ
+        L.oracle_softmax.argtypes = [_F, _SZ, _SZ, _F]
+        L.oracle_softmax_backward.argtypes = [_F, _F, _SZ, _SZ, _F]
+        MT = ctypes.c_void_p
+        L.oracle_mt_seed.argtypes = [MT, ctypes.c_uint64]
+        L.oracle_mt_random.argtypes = [MT, ctypes.POINTER(ctypes.c_uint32), _SZ]
+        L.oracle_mt_uniform_f64.argtypes = [MT, ctypes.POINTER(ctypes.c_double), _SZ]
+        L.oracle_mt_bernoulli.argtypes = [MT, ctypes.c_double, _F, _SZ]
         _lib = L
     return _lib
 
@@ -285,3 +292,57 @@ def math_attention(query, key, value, attn_mask=None, is_causal=False, scale=Non
     dqs = bmm(da, ks)
     dks = bmm(np.swapaxes(da, -1, -2), qs)
     return out, (dqs * fq, dks * fk, dv, da)
+
+
+# ---- the reference's generator (src/torch_random.rs:9-110, 241-254), one output at a time ----
+
+class _MT(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_uint32 * 624), ("left", ctypes.c_int64), ("next", ctypes.c_int64)]
+
+
+class Generator:
+    """``torch_random::Generator``'s engine and the draws the dropout path uses."""
+
+    def __init__(self, seed=67_280_421_310_721):
+        self._g = _MT()
+        self.manual_seed(seed)
+
+    def manual_seed(self, seed):
+        lib().oracle_mt_seed(ctypes.addressof(self._g), int(seed) & (2**64 - 1))
+
+    @property
+    def words(self):
+        return np.frombuffer(self._g.state, np.uint32).copy()
+
+    @property
+    def position(self):
+        return int(self._g.left), int(self._g.next)
+
+    def set(self, words, left, next_):
+        self._g.state[:] = [int(w) for w in np.asarray(words, np.uint32)]
+        self._g.left, self._g.next = int(left), int(next_)
+
+    def random(self, n):
+        out = np.empty(int(n), np.uint32)
+        lib().oracle_mt_random(ctypes.addressof(self._g), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                               out.size)
+        return out
+
+    def uniform_doubles(self, n):
+        out = np.empty(int(n), np.float64)
+        lib().oracle_mt_uniform_f64(ctypes.addressof(self._g),
+                                    out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), out.size)
+        return out
+
+    def bernoulli(self, n, p):
+        """``Generator::bernoulli(n, p)``: float32 0/1."""
+        out = np.empty(int(n), np.float32)
+        lib().oracle_mt_bernoulli(ctypes.addressof(self._g), float(p), _p(out), out.size)
+        return out
+
+
+def dropout_noise(gen, shape, p):
+    """``_dropout_noise`` (``python/densecore/functional.py:638-641``): bernoulli(1 - p) divided
+    by float32(1 - p), in float32."""
+    n = int(np.prod(shape))
+    return (gen.bernoulli(n, 1 - p) / np.float32(1 - p)).reshape(shape)

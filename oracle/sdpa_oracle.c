@@ -20,6 +20,8 @@
  *   src/torch_sum.rs:17-68          thread count (splits work only; never changes bits)
  *   src/torch_softmax.rs:57-67,90-97  softmax_lastdim / softmax_backward_lastdim (the math
  *                                   path's Tensor.softmax(-1) and its gradient)
+ *   src/torch_random.rs:9-110,241-254 the generator (PyTorch's mt19937: manual_seed, twist,
+ *                                   random, random64, uniform_f64) and bernoulli, sequential
  *
  * Build flags matter: -O2 -ffp-contract=off -fno-fast-math.  Rust never contracts a*b+c,
  * so every explicit Rust `mul_add` is an explicit fmaf here and nothing else is fused.
@@ -539,6 +541,67 @@ EXPORT void oracle_softmax_backward(const float *g, const float *y, size_t rows,
         const float sum = reduce_all_dot(gr, yr, width);
         for (size_t i = 0; i < width; ++i) dx[r * width + i] = (gr[i] - sum) * yr[i];
     }
+}
+
+/* ---- torch_random.rs:9-110, 241-254: the reference's generator, one output at a time ---- */
+typedef struct {
+    uint32_t state[624];
+    int64_t left, next;
+} mt_t;
+
+static uint32_t mt_twist(uint32_t u, uint32_t v) {
+    return (((u & 0x80000000u) | (v & 0x7fffffffu)) >> 1) ^ ((v & 1u) ? 0x9908b0dfu : 0u);
+}
+
+/* manual_seed, torch_random.rs:43-56 */
+EXPORT void oracle_mt_seed(mt_t *g, uint64_t seed) {
+    g->state[0] = (uint32_t)seed;
+    for (int j = 1; j < 624; ++j)
+        g->state[j] = 1812433253u * (g->state[j - 1] ^ (g->state[j - 1] >> 30)) + (uint32_t)j;
+    g->left = 1;
+    g->next = 0;
+}
+
+/* next_state, torch_random.rs:66-77 (in place, three loops) */
+static void mt_next_state(mt_t *g) {
+    uint32_t *s = g->state;
+    g->left = 624;
+    g->next = 0;
+    for (int j = 0; j < 624 - 397; ++j) s[j] = s[j + 397] ^ mt_twist(s[j], s[j + 1]);
+    for (int j = 624 - 397; j < 623; ++j) s[j] = s[j + 397 - 624] ^ mt_twist(s[j], s[j + 1]);
+    s[623] = s[396] ^ mt_twist(s[623], s[0]);
+}
+
+/* random, torch_random.rs:79-91 */
+static uint32_t mt_random(mt_t *g) {
+    if (--g->left == 0) mt_next_state(g);
+    uint32_t y = g->state[g->next++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+/* uniform_f64(0, 1), torch_random.rs:93-110: random64 = hi << 32 | lo, 53 bits, then
+ * mul_add(1 - 0, 0) which leaves the product unchanged. */
+static double mt_uniform_f64(mt_t *g) {
+    const uint64_t hi = mt_random(g), lo = mt_random(g);
+    const uint64_t r = ((hi << 32) | lo) & ((1ull << 53) - 1);
+    return fma((double)r * (1.0 / (double)(1ull << 53)), 1.0, 0.0);
+}
+
+EXPORT void oracle_mt_random(mt_t *g, uint32_t *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = mt_random(g);
+}
+
+EXPORT void oracle_mt_uniform_f64(mt_t *g, double *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = mt_uniform_f64(g);
+}
+
+/* bernoulli, torch_random.rs:241-254: 1.0 where the double uniform is below p. */
+EXPORT void oracle_mt_bernoulli(mt_t *g, double p, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = mt_uniform_f64(g) < p ? 1.0f : 0.0f;
 }
 
 /* ---- thread count, torch_sum.rs:51-68 ---- */
