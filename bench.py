@@ -1,6 +1,6 @@
 """Benchmark of the SDPA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only C2,C4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only C2,C4,math]
 
 A step is one pass of the hot path over one batch of synthetic, HBM-resident input:
 C2 (the headline) is causal fp32 forward + backward at B8 H12 T1024
@@ -10,6 +10,8 @@ metric names (C4, dc_sdpa_decode, GB/s of K + V + q + out + lse), the other conf
 throughput (wall clock over K steps between two synchronizations), a roofline entry per
 entry point whose kernel time comes from HIP events on the launch stream around back-to-back
 calls of that entry point alone, and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
+``math_path`` reports the composed path's own kernels (softmax forward/backward, the Bernoulli
+mask from the reference's generator stream, the dropout product) at C3's shape.
 """
 import argparse
 import json
@@ -140,6 +142,67 @@ def bench_decode(torch, native, steps, warmup, dev):
             "gbps": nbytes / (ev * 1e-3) / 1e9}
 
 
+def bench_math(torch, steps, warmup, dev):
+    """The composed math path's own kernels at C3's shape (B16 H16 L=S=512, key-padding mask)
+    with dropout p = 0.1: softmax forward (scores + broadcast mask -> probabilities, 8 B per
+    score) and backward (12 B per score) against HBM, the Bernoulli mask drawn from the
+    reference's generator stream (draws/s), the dropout product (8 B per score plus the bits),
+    and one whole math-path step (forward + backward through autograd, the two batched
+    products on the device BLAS)."""
+    import densecore_amd._native as native
+    from densecore_amd import functional as F, random as R
+    from tests._data import CONFIGS, additive, make_inputs
+    B, H, L, S, E, _, _, _ = CONFIGS["C3"]
+    d = make_inputs("C3")
+    n = B * H * L * S
+    stream = torch.cuda.current_stream(dev)
+    x = torch.randn((B, H, L, S), device=dev)
+    mask = torch.from_numpy(additive(d["mask_bool"], (B, 1, 1, S)).copy()).to(dev)
+    y = native._softmax(x, mask, True)
+    g = torch.randn_like(x)
+    reps = max(steps, 10)
+    for _ in range(warmup):
+        native._softmax(x, mask, True)
+    res = {"workload": "C3 shape B16 H16 L=S=512, key-padding mask, dropout p=0.1",
+           "timing_calls": reps}
+    ms = kernel_ms(torch, stream, lambda: native._softmax(x, mask, True), reps)
+    res["softmax_fwd"] = {"ms": round(ms, 4), "gbps": round(8 * n / (ms * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(8 * n / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    ms = kernel_ms(torch, stream, lambda: native._softmax_backward(g, y), reps)
+    res["softmax_bwd"] = {"ms": round(ms, 4), "gbps": round(12 * n / (ms * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(12 * n / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    gen = R.Generator(dev).manual_seed(0)
+    gen._bernoulli_bits(n, 0.9)
+    ms = kernel_ms(torch, stream, lambda: gen._bernoulli_bits(n, 0.9), reps)
+    res["bernoulli"] = {"ms": round(ms, 4), "gdraws_per_s": round(n / (ms * 1e-3) / 1e9, 2),
+                        "mt19937_words_per_s_g": round(2 * n / (ms * 1e-3) / 1e9, 2)}
+    bits = gen._bernoulli_bits(n, 0.9)
+    scale = float(np.float32(1) / np.float32(0.9))
+    ms = kernel_ms(torch, stream, lambda: native._dropout_apply(bits, y, scale), reps)
+    nb = 8 * n + n // 8
+    res["dropout_apply"] = {"ms": round(ms, 4), "gbps": round(nb / (ms * 1e-3) / 1e9, 1),
+                            "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    del x, y, g, bits
+    q, k, v = (torch.from_numpy(d[c]).to(dev).requires_grad_(True) for c in "qkv")
+    am = torch.from_numpy(d["mask_bool"]).to(dev)
+    go = torch.randn((B, H, L, E), device=dev)
+
+    def step():
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=am, dropout_p=0.1)
+        out.backward(go)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    k_steps = max(3, steps // 10)
+    for _ in range(k_steps):
+        step()
+    torch.cuda.synchronize()
+    res["math_path_step_ms"] = round((time.perf_counter() - t0) / k_steps * 1e3, 3)
+    return res
+
+
 def cpu_baseline(threads):
     """The oracle (C port of DenseCore's CPU SDPA) on the full C2 workload, this host's cores."""
     import oracle
@@ -167,7 +230,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of configs to run (C1..C5)")
+    ap.add_argument("--only", default="", help="comma list of configs to run (C1..C5, math)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (torch copy_), the kernel "
                          "of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -203,6 +266,9 @@ def main():
         torch.cuda.empty_cache()
     if "C4" in only:
         results["C4"] = bench_decode(torch, native, args.steps, args.warmup, dev)
+        torch.cuda.empty_cache()
+    if "math" in only or not args.only:
+        results["math"] = bench_math(torch, args.steps, args.warmup, dev)
         torch.cuda.empty_cache()
 
     traffic = load_traffic()
@@ -252,6 +318,8 @@ def main():
             others[name]["bwd_ms"] = round(r["bwd_ms"], 4)
     if others:
         line["other_configs"] = others
+    if results.get("math"):
+        line["math_path"] = results["math"]
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         line["cpu_baseline"] = cpu_baseline(threads)

@@ -359,7 +359,7 @@ dc_status dc_bernoulli(const void *table, uint32_t *state, int64_t *left, int64_
     a.bits = keep_bits;
     a.win = static_cast<uint32_t *>(workspace);
     a.n = n;
-    a.p = p;
+    a.thr = (uint64_t)std::ceil(p * 0x1p53);  // exact: p in [0, 1], scaled by a power of two
     a.r = (int)r;
     a.eh = dc::mt::kHead;
     a.a0 = a.r + 2 * a.eh;

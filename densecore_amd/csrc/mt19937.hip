@@ -17,16 +17,16 @@
 //             (mt_base_kernel), which also writes the window at A0 = r + 2 Eh (A0 >= 1, so that
 //             window follows an update even when the block is a freshly seeded one);
 //   chunks    chunk c covers elements [Eh + c J/2, Eh + (c + 1) J/2), J = 2^17 words; its window
-//             is W(A0 + c J), reached from W(A0) through a radix-16 tree of jumps (c = 256 c3 +
-//             16 c2 + c1: jumps by c3 2^25, then c2 2^21, then c1 2^17; mt_jump_kernel), and
-//             one wave generates its words from that window (mt_chunk_kernel).
+//             is W(A0 + c J), reached from W(A0) through a radix-64 tree of jumps (c = 64 c1 + c0:
+//             a jump by c1 2^23, then one by c0 2^17; mt_jump_kernel), and one wave generates its
+//             words from that window (mt_chunk_kernel).
 // Keep bits: element e is bit e % 32 of word e / 32 (heads and chunks write whole words).  The
 // engine block that holds the last output drawn is written back to the state (by the base
 // workgroup or by the chunk whose range holds the block's first word), and the host moves
 // (left, next) the way next_state/random do.
 //
-// The jump polynomials (48 of them) are computed once on the host: phi by Berlekamp-Massey on
-// 2 * 19937 bits of the stream, then z^(digit * 2^(17 + 4 level)) mod phi by squaring and
+// The jump polynomials (128 of them) are computed once on the host: phi by Berlekamp-Massey on
+// 2 * 19937 bits of the stream, then z^(digit * 2^(17 + 6 level)) mod phi by squaring and
 // multiplying; the caller uploads them into its own device buffer (dc_mt19937_table_init).
 #include <cstring>
 #include <mutex>
@@ -206,11 +206,21 @@ DEVI uint32_t temper(uint32_t y) {
     return y;
 }
 
-// uniform_f64 (src/torch_random.rs:106-110) of the pair (hi, lo) compared with p: the product
-// is exact, and mul_add(1, 0) leaves it unchanged.
-DEVI bool keep(uint32_t hi, uint32_t lo, double p) {
+// uniform_f64 (src/torch_random.rs:106-110) of the pair (hi, lo) compared with p: with
+// r = (hi << 32 | lo) & (2^53 - 1), r * 2^-53 < p exactly when r < ceil(p * 2^53) (both sides
+// scaled by a power of two, r an integer), the threshold the host computes.
+DEVI bool keep(uint32_t hi, uint32_t lo, uint64_t thr) {
     const uint64_t r = (((uint64_t)hi << 32) | lo) & ((1ull << 53) - 1);
-    return (double)r * 0x1p-53 < p;
+    return r < thr;
+}
+
+// Orders this wave's LDS accesses around it (the LDS executes one wave's instructions in order,
+// so the compiler is the only thing that could move a read above another lane's write): the
+// wave-scope release / wave barrier / acquire sequence, no wait on global stores.
+DEVI void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // One workgroup: the current block `state` (positions 0..623), the words after it up to
@@ -235,7 +245,7 @@ __global__ __launch_bounds__(256) void mt_base_kernel(MtArgs a) {
     for (int e0 = wave * 64; e0 < a.eh; e0 += 256) {
         const int e = e0 + lane;
         bool k = false;
-        if (e < head) k = keep(temper(x[a.r + 2 * e]), temper(x[a.r + 2 * e + 1]), a.p);
+        if (e < head) k = keep(temper(x[a.r + 2 * e]), temper(x[a.r + 2 * e + 1]), a.thr);
         const uint64_t m = __ballot(k);
         if (e0 < head) {
             if (lane == 0) a.bits[e0 >> 5] = (uint32_t)m;
@@ -247,16 +257,20 @@ __global__ __launch_bounds__(256) void mt_base_kernel(MtArgs a) {
         for (int i = tid; i < kState; i += 256) a.state[i] = x[a.state_block * kState + i];
 }
 
-// One workgroup per destination window: dst[w] = W(src[w / 16] + digit * step), digit = w % 16,
-// with g = table[level][digit].  Threads t < 78 own output words 8t .. 8t + 7 and slide an
-// 8-word register window along the sequence, which is generated into an LDS ring 1024 words
-// ahead of the sum.
-constexpr int kRing = 2048;
-constexpr int kSeg = 1024;
+// One workgroup per destination window: dst[w] = W(src[w / 64] + digit * step), digit = w % 64,
+// with g = table[level][digit].  The sequence seq[i] = x[src + i], i < 20576, is generated into
+// LDS once; wave v sums the g-terms of i in its eighth of [0, 19937): lanes < 52 own 12
+// consecutive output words each and slide a 20-word register window along seq, 8 terms per
+// step; the eight partial windows are then XORed together.
+constexpr int kSeqWords = 20576;                        // >= 19937 + 624 + 15, a multiple of 8
+constexpr int kJumpWaves = 8;
+constexpr int kGroups = (kDegree + 7) / 8;              // groups of 8 terms
+constexpr int kGroupsPerWave = (kGroups + kJumpWaves - 1) / kJumpWaves;
+constexpr int kOwn = 12, kOwners = kState / kOwn;       // 52 owner lanes per wave
 
-__global__ __launch_bounds__(128) void mt_jump_kernel(const uint32_t *src, uint32_t *dst,
+__global__ __launch_bounds__(512) void mt_jump_kernel(const uint32_t *src, uint32_t *dst,
                                                       const uint32_t *table, int level, int count) {
-    __shared__ uint32_t ring[kRing];
+    __shared__ __align__(16) uint32_t seq[kSeqWords];
     const int w = blockIdx.x;
     if (w >= count) return;
     const int digit = w % kRadix;
@@ -264,53 +278,58 @@ __global__ __launch_bounds__(128) void mt_jump_kernel(const uint32_t *src, uint3
     uint32_t *out = dst + (size_t)w * kState;
     const int tid = threadIdx.x;
     if (digit == 0) {
-        for (int i = tid; i < kState; i += 128) out[i] = in[i];
+        for (int i = tid; i < kState; i += 512) out[i] = in[i];
         return;
     }
     const uint32_t *g = table + ((size_t)level * kRadix + digit) * kTableWords;
-    for (int i = tid; i < kState; i += 128) ring[i] = in[i];
-    int made = kState;
-    uint32_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const bool owner = tid < kState / 8;
-    for (int seg = 0; seg < kDegree; seg += kSeg) {
-        const int seg_end = seg + kSeg < kDegree + 7 ? seg + kSeg : kDegree + 7;  // i < seg_end
-        const int need = (seg_end + 7) / 8 * 8 + kState + 8;  // words read by this segment
+    for (int i = tid; i < kState; i += 512) seq[i] = in[i];
+    __syncthreads();
+    for (int base = kState; base < kSeqWords; base += 227) {  // x[u] needs x[u - 227]: 227 at a time
+        const int u = base + tid;
+        if (tid < 227 && u < kSeqWords) seq[u] = seq[u - 227] ^ twist_d(seq[u - 624], seq[u - 623]);
         __syncthreads();
-        while (made < need) {
-            const int u = made + tid;
-            if (u < need)
-                ring[u & (kRing - 1)] = ring[(u - 227) & (kRing - 1)] ^
-                                        twist_d(ring[(u - 624) & (kRing - 1)], ring[(u - 623) & (kRing - 1)]);
-            made = made + 128 < need ? made + 128 : need;  // the next segment continues at `need`
-            __syncthreads();
-        }
-        if (owner) {
-            const int j0 = 8 * tid;
-            uint32_t cur[8];
+    }
+    const int wave = tid >> 6, lane = tid & 63;
+    uint32_t acc[kOwn];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) cur[u] = ring[(seg + j0 + u) & (kRing - 1)];
-            for (int i0 = seg; i0 < seg_end; i0 += 8) {
-                uint32_t nxt[8];
+    for (int u = 0; u < kOwn; ++u) acc[u] = 0;
+    if (lane < kOwners) {
+        const int j0 = kOwn * lane;
+        const int g_begin = wave * kGroupsPerWave;
+        const int g_end = g_begin + kGroupsPerWave < kGroups ? g_begin + kGroupsPerWave : kGroups;
+        uint32_t cur[kOwn];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) nxt[u] = ring[(i0 + 8 + j0 + u) & (kRing - 1)];
-                const uint32_t gb = (g[i0 >> 5] >> (i0 & 31)) & 0xffu;  // g bits i0 .. i0 + 7
-                if (gb) {
+        for (int u = 0; u < kOwn; ++u) cur[u] = seq[8 * g_begin + j0 + u];
+        for (int gi = g_begin; gi < g_end; ++gi) {
+            const int i0 = 8 * gi;
+            uint32_t nxt[8];
 #pragma unroll
-                    for (int d = 0; d < 8; ++d) {
-                        if (gb >> d & 1u) {
+            for (int u = 0; u < 8; ++u) nxt[u] = seq[i0 + j0 + kOwn + u];
+            const uint32_t gb = (g[i0 >> 5] >> (i0 & 31)) & 0xffu;  // g bits i0 .. i0 + 7
+            if (gb) {
 #pragma unroll
-                            for (int u = 0; u < 8; ++u) acc[u] ^= (d + u < 8) ? cur[d + u] : nxt[d + u - 8];
-                        }
+                for (int d = 0; d < 8; ++d) {
+                    if (gb >> d & 1u) {
+#pragma unroll
+                        for (int u = 0; u < kOwn; ++u) acc[u] ^= (d + u < kOwn) ? cur[d + u] : nxt[d + u - kOwn];
                     }
                 }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
             }
+#pragma unroll
+            for (int u = 0; u < kOwn; ++u) cur[u] = u + 8 < kOwn ? cur[u + 8] : nxt[u + 8 - kOwn];
         }
     }
-    if (owner)
+    __syncthreads();  // every wave is done with seq: reuse it for the partial windows
+    if (lane < kOwners)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) out[8 * tid + u] = acc[u];
+        for (int u = 0; u < kOwn; ++u) seq[wave * kState + kOwn * lane + u] = acc[u];
+    __syncthreads();
+    for (int j = tid; j < kState; j += 512) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int v = 0; v < kJumpWaves; ++v) x ^= seq[v * kState + j];
+        out[j] = x;
+    }
 }
 
 // One wave per chunk: words A0 + c J .. from its window, 64 elements (128 words) per step.
@@ -320,6 +339,7 @@ __global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *
     const int lane = threadIdx.x;
     const uint32_t *win = wins + (size_t)c * kState;
     for (int i = lane; i < kState; i += 64) ring[i] = win[i];
+    wave_lds_order();
     const int64_t e_begin = a.eh + (int64_t)c * (kChunkWords / 2);
     int64_t e_end = e_begin + kChunkWords / 2;
     if (e_end > a.n) e_end = a.n;
@@ -330,7 +350,6 @@ __global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *
                               sb >= 0 && sb < kChunkWords;
     const int64_t words = writes_state && sb + kState > 2 * (e_end - e_begin)
                               ? sb + kState : 2 * (e_end - e_begin);
-    __syncthreads();
     for (int64_t base = 0; base < words; base += 128) {
         const int u0 = (int)base + 2 * lane;
         uint32_t w0, w1;
@@ -344,14 +363,14 @@ __global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *
             ring[(u0 + 1) & 1023] = w1;
         }
         const int64_t e = e_begin + base / 2 + lane;
-        const bool k = e < e_end && keep(temper(w0), temper(w1), a.p);
+        const bool k = e < e_end && keep(temper(w0), temper(w1), a.thr);
         const uint64_t m = __ballot(k);
         const int64_t e0 = e_begin + base / 2;
         if (e0 < e_end) {
             if (lane == 0) a.bits[e0 >> 5] = (uint32_t)m;
             if (lane == 1 && e0 + 32 < e_end) a.bits[(e0 >> 5) + 1] = (uint32_t)(m >> 32);
         }
-        __syncthreads();
+        wave_lds_order();
         if (writes_state && base + 128 >= sb + kState && base < sb + kState) {
             // Words sb .. sb + 623 are the last <= 752 words made: all still in the ring.
             for (int i = lane; i < kState; i += 64) a.state[i] = ring[(sb + i) & 1023];
@@ -360,7 +379,8 @@ __global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *
 }
 
 // y = x * (keep ? scale : 0): the reference's input * noise, noise = bernoulli / float32(1 - p)
-// (python/densecore/functional.py:244, 638-641).
+// (python/densecore/functional.py:244, 638-641).  Four elements per thread (one 16-byte load
+// and store, four bits of one word) when the tensors allow it.
 __global__ __launch_bounds__(256) void dropout_apply_kernel(const uint32_t *bits, int64_t n, float scale,
                                                             const float *x, float *y) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -369,13 +389,23 @@ __global__ __launch_bounds__(256) void dropout_apply_kernel(const uint32_t *bits
     y[i] = x[i] * (k ? scale : 0.0f);
 }
 
+__global__ __launch_bounds__(256) void dropout_apply4_kernel(const uint32_t *bits, int64_t n4, float scale,
+                                                             const f32x4 *x, f32x4 *y) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= n4) return;
+    const uint32_t b = bits[t >> 3] >> (4 * (t & 7));
+    f32x4 v = x[t];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = v[c] * ((b >> c & 1u) ? scale : 0.0f);
+    y[t] = v;
+}
+
 }  // namespace
 
 size_t window_words(int chunks) {
     if (chunks == 0) return kState;
-    const int n3 = (chunks + kRadix * kRadix - 1) / (kRadix * kRadix);
-    const int n2 = (chunks + kRadix - 1) / kRadix;
-    return (size_t)(1 + n3 + n2 + chunks) * kState;
+    const int n1 = (chunks + kRadix - 1) / kRadix;
+    return (size_t)(1 + n1 + chunks) * kState;
 }
 
 bool tables_ready() { return tables().ok; }
@@ -400,21 +430,23 @@ hipError_t launch_bernoulli(const MtArgs &a, const uint32_t *table, int chunks, 
                             hipStream_t st) {
     return_if(launch(mt_base_kernel, dim3(1), dim3(256), st, a));
     if (chunks == 0) return hipSuccess;
-    // Radix-16 tree: level 2 (c3), level 1 (c2), level 0 (c1).  Window arrays are carved from
-    // `wins` (window_words(chunks) words): [W(A0)] [n3 level-2] [n2 level-1] [chunks].
-    const int n3 = (chunks + kRadix * kRadix - 1) / (kRadix * kRadix);
-    const int n2 = (chunks + kRadix - 1) / kRadix;
-    uint32_t *l3 = wins + kState, *l2 = l3 + (size_t)n3 * kState, *l1 = l2 + (size_t)n2 * kState;
-    return_if(launch(mt_jump_kernel, dim3(n3), dim3(128), st, (const uint32_t *)wins, l3, table, 2, n3));
-    return_if(launch(mt_jump_kernel, dim3(n2), dim3(128), st, (const uint32_t *)l3, l2, table, 1, n2));
-    return_if(launch(mt_jump_kernel, dim3(chunks), dim3(128), st, (const uint32_t *)l2, l1, table, 0, chunks));
-    return launch(mt_chunk_kernel, dim3(chunks), dim3(64), st, a, (const uint32_t *)l1);
+    // Radix-64 tree: level 1 (c1), then level 0 (c0).  Window arrays are carved from `wins`
+    // (window_words(chunks) words): [W(A0)] [n1 level-1 windows] [chunk windows].
+    const int n1 = (chunks + kRadix - 1) / kRadix;
+    uint32_t *l1 = wins + kState, *l0 = l1 + (size_t)n1 * kState;
+    return_if(launch(mt_jump_kernel, dim3(n1), dim3(512), st, (const uint32_t *)wins, l1, table, 1, n1));
+    return_if(launch(mt_jump_kernel, dim3(chunks), dim3(512), st, (const uint32_t *)l1, l0, table, 0, chunks));
+    return launch(mt_chunk_kernel, dim3(chunks), dim3(64), st, a, (const uint32_t *)l0);
 }
 
 hipError_t launch_dropout_apply(const uint32_t *bits, int64_t n, float scale, const float *x, float *y,
                                 hipStream_t st) {
-    const int64_t blocks = (n + 255) / 256;
-    return launch(dropout_apply_kernel, dim3((unsigned)blocks), dim3(256), st, bits, n, scale, x, y);
+    if (n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0) {
+        const int64_t n4 = n / 4;
+        return launch(dropout_apply4_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, bits, n4,
+                      scale, reinterpret_cast<const f32x4 *>(x), reinterpret_cast<f32x4 *>(y));
+    }
+    return launch(dropout_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), st, bits, n, scale, x, y);
 }
 
 }  // namespace mt

@@ -70,17 +70,17 @@ hipError_t launch_softmax_bwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
 namespace mt {
 constexpr int kState = 624, kM = 397, kDegree = 19937;
 constexpr int kTableWords = 624;  // uint32 words per jump polynomial (19968 bits)
-constexpr int kRadix = 16, kJumpLevels = 3, kTablePolys = kRadix * kJumpLevels;
+constexpr int kRadix = 64, kJumpLevels = 2, kTablePolys = kRadix * kJumpLevels;
 constexpr int kChunkLog2 = 17, kChunkWords = 1 << kChunkLog2;  // words per chunk (one wave)
 constexpr int kHead = 64;                                       // elements of the base workgroup
-constexpr int kMaxChunks = kRadix * kRadix * kRadix;
+constexpr int kMaxChunks = kRadix * kRadix;
 
 struct MtArgs {
     uint32_t *state;      // the engine block (624 words), in/out
     uint32_t *bits;       // keep bits, element e = bit e % 32 of word e / 32
     uint32_t *win;        // out: the window at A0
     int64_t n;            // elements
-    double p;             // keep iff uniform double < p
+    uint64_t thr;         // keep iff the 53-bit integer r < thr = ceil(p * 2^53) (r * 2^-53 < p)
     int r, a0, eh;        // first output, first chunk word (relative to the block), head elements
     int64_t state_block;  // block (relative) holding the last output, or -1 when n == 0
 };
