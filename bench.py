@@ -204,9 +204,11 @@ def bench_math(torch, steps, warmup, dev):
 
 
 def cpu_baseline(threads):
-    """The oracle (C port of DenseCore's CPU SDPA) on the full C2 workload, this host's cores."""
+    """The oracle (C port of DenseCore's CPU SDPA) on this host's cores: the full C2 workload
+    (the headline figure, median of 2) and, once each, full C1, C3 (the reference's materialised
+    (B, H, L, S) mask) and C4, in the units of their GPU figures."""
     import oracle
-    from tests._data import make_inputs
+    from tests._data import additive, make_inputs
     oracle.build()
     oracle.set_num_threads(threads)
     d = make_inputs("C2")
@@ -218,10 +220,31 @@ def cpu_baseline(threads):
         times.append(time.perf_counter() - t0)
     ff, fb = flops(8, 12, 1024, 1024, 64, True, True)
     best = float(np.median(times))
+    per = {}
+    d = make_inputs("C1")
+    t0 = time.perf_counter()
+    oracle.forward(d["q"], d["k"], d["v"], True)
+    dt = time.perf_counter() - t0
+    per["C1"] = {"tflops": round(flops(64, 6, 256, 256, 64, True, False)[0] / dt / 1e12, 5),
+                 "s": round(dt, 3)}
+    d = make_inputs("C3")
+    mask = additive(d["mask_bool"], (16, 16, 512, 512))
+    t0 = time.perf_counter()
+    oracle.forward(d["q"], d["k"], d["v"], False, None, mask)
+    dt = time.perf_counter() - t0
+    per["C3"] = {"tflops": round(4.0 * 16 * 512 * 64 * float(np.sum(d["lengths"])) / dt / 1e12, 5),
+                 "s": round(dt, 3), "note": "useful FLOPs (valid keys); the CPU path computes every key"}
+    del mask
+    d = make_inputs("C4")
+    t0 = time.perf_counter()
+    oracle.forward(d["q"], d["k"], d["v"], False)
+    dt = time.perf_counter() - t0
+    per["C4"] = {"gbps": round(decode_bytes(32, 32, 4096, 128) / dt / 1e9, 2), "s": round(dt, 3)}
     return {"value": round((ff + fb) / best / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"full C2 fwd+bwd (B8 H12 T1024 D64 fp32) x{len(times)}, median "
-                      f"{best:.2f} s; oracle/sdpa_oracle.c, {threads} threads"}
+                      f"{best:.2f} s; oracle/sdpa_oracle.c, {threads} threads",
+            "configs": per}
 
 
 def main():
