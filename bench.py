@@ -206,7 +206,8 @@ def bench_math(torch, steps, warmup, dev):
 def cpu_baseline(threads):
     """The oracle (C port of DenseCore's CPU SDPA) on this host's cores: the full C2 workload
     (the headline figure, median of 2) and, once each, full C1, C3 (the reference's materialised
-    (B, H, L, S) mask) and C4, in the units of their GPU figures."""
+    (B, H, L, S) mask) and C4, in the units of their GPU figures, plus the math path's softmax
+    and Bernoulli draws on a slice of C3's shape."""
     import oracle
     from tests._data import additive, make_inputs
     oracle.build()
@@ -240,6 +241,21 @@ def cpu_baseline(threads):
     oracle.forward(d["q"], d["k"], d["v"], False)
     dt = time.perf_counter() - t0
     per["C4"] = {"gbps": round(decode_bytes(32, 32, 4096, 128) / dt / 1e9, 2), "s": round(dt, 3)}
+    # The math path's pieces at C3's shape, single-threaded as the reference runs them:
+    # softmax_lastdim over 8 of the 256 (b, h) score blocks and Generator::bernoulli draws.
+    x = np.random.default_rng(0).standard_normal((8, 512, 512), dtype=np.float32)
+    t0 = time.perf_counter()
+    oracle.softmax(x)
+    dt = time.perf_counter() - t0
+    n = 16 * 16 * 512 * 512 // 8
+    gen = oracle.Generator(0)
+    t1 = time.perf_counter()
+    gen.bernoulli(n, 0.9)
+    db = time.perf_counter() - t1
+    per["math_path"] = {"softmax_gbps": round(8 * x.size / dt / 1e9, 3),
+                        "bernoulli_gdraws_per_s": round(n / db / 1e9, 4), "threads": 1,
+                        "sample": f"softmax of {x.size} scores (8 of C3's 256 blocks, {dt:.3f} s), "
+                                  f"{n} Bernoulli draws (an eighth of C3's, {db:.3f} s)"}
     return {"value": round((ff + fb) / best / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"full C2 fwd+bwd (B8 H12 T1024 D64 fp32) x{len(times)}, median "
