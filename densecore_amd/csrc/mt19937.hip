@@ -260,8 +260,8 @@ __global__ __launch_bounds__(256) void mt_base_kernel(MtArgs a) {
 // One workgroup per destination window: dst[w] = W(src[w / 64] + digit * step), digit = w % 64,
 // with g = table[level][digit].  The sequence seq[i] = x[src + i], i < 20576, is generated into
 // LDS once; wave v sums the g-terms of i in its eighth of [0, 19937): lanes < 52 own 12
-// consecutive output words each and slide a 20-word register window along seq, 8 terms per
-// step; the eight partial windows are then XORed together.
+// consecutive output words each and read a 20-word window of seq per group of 8 terms; the
+// eight partial windows are then XORed together.
 constexpr int kSeqWords = 20576;                        // >= 19937 + 624 + 15, a multiple of 8
 constexpr int kJumpWaves = 8;
 constexpr int kGroups = (kDegree + 7) / 8;              // groups of 8 terms
@@ -289,40 +289,43 @@ __global__ __launch_bounds__(512) void mt_jump_kernel(const uint32_t *src, uint3
         if (tid < 227 && u < kSeqWords) seq[u] = seq[u - 227] ^ twist_d(seq[u - 624], seq[u - 623]);
         __syncthreads();
     }
-    const int wave = tid >> 6, lane = tid & 63;
+    // Every lane runs the sum (lanes past the owners repeat the last owner's words and store
+    // nothing), so the group index and the polynomial bits are wave-uniform: the bits come from
+    // two VGPRs loaded up front (word w of this wave's 78 at lane w % 64 of gw[w / 64]) through
+    // readlane, and the term tests are scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int j0 = kOwn * (lane < kOwners ? lane : kOwners - 1);
+    const int g_begin = wave * kGroupsPerWave;
+    const int g_end = g_begin + kGroupsPerWave < kGroups ? g_begin + kGroupsPerWave : kGroups;
+    static_assert(kGroupsPerWave % 4 == 0 && kGroupsPerWave / 4 <= 128, "g words per wave");
+    const int w0 = g_begin / 4;  // first g word of this wave (4 groups of 8 bits per word)
+    const uint32_t gw0 = w0 + lane < kTableWords ? g[w0 + lane] : 0u;
+    const uint32_t gw1 = w0 + 64 + lane < kTableWords ? g[w0 + 64 + lane] : 0u;
     uint32_t acc[kOwn];
 #pragma unroll
     for (int u = 0; u < kOwn; ++u) acc[u] = 0;
-    if (lane < kOwners) {
-        const int j0 = kOwn * lane;
-        const int g_begin = wave * kGroupsPerWave;
-        const int g_end = g_begin + kGroupsPerWave < kGroups ? g_begin + kGroupsPerWave : kGroups;
-        uint32_t cur[kOwn];
+    for (int gi = g_begin; gi < g_end; ++gi) {
+        const int wi = (gi >> 2) - w0;
+        const uint32_t word = wi < 64 ? __builtin_amdgcn_readlane(gw0, wi)
+                                      : __builtin_amdgcn_readlane(gw1, wi - 64);
+        const uint32_t gb = (word >> (8 * (gi & 3))) & 0xffu;  // g bits 8 gi .. 8 gi + 7
+        if (gb == 0) continue;
+        uint32_t win[kOwn + 8];  // seq[8 gi + j0 + 0 .. 19]: five 16-byte reads
 #pragma unroll
-        for (int u = 0; u < kOwn; ++u) cur[u] = seq[8 * g_begin + j0 + u];
-        for (int gi = g_begin; gi < g_end; ++gi) {
-            const int i0 = 8 * gi;
-            uint32_t nxt[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) nxt[u] = seq[i0 + j0 + kOwn + u];
-            const uint32_t gb = (g[i0 >> 5] >> (i0 & 31)) & 0xffu;  // g bits i0 .. i0 + 7
-            if (gb) {
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    if (gb >> d & 1u) {
-#pragma unroll
-                        for (int u = 0; u < kOwn; ++u) acc[u] ^= (d + u < kOwn) ? cur[d + u] : nxt[d + u - kOwn];
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kOwn; ++u) cur[u] = u + 8 < kOwn ? cur[u + 8] : nxt[u + 8 - kOwn];
+        for (int u = 0; u < kOwn + 8; u += 4) {
+            const u32x4 x = *reinterpret_cast<const u32x4 *>(&seq[8 * gi + j0 + u]);
+            win[u] = x[0], win[u + 1] = x[1], win[u + 2] = x[2], win[u + 3] = x[3];
         }
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+            if (gb >> d & 1u)
+#pragma unroll
+                for (int u = 0; u < kOwn; ++u) acc[u] ^= win[d + u];
     }
     __syncthreads();  // every wave is done with seq: reuse it for the partial windows
     if (lane < kOwners)
 #pragma unroll
-        for (int u = 0; u < kOwn; ++u) seq[wave * kState + kOwn * lane + u] = acc[u];
+        for (int u = 0; u < kOwn; ++u) seq[wave * kState + j0 + u] = acc[u];
     __syncthreads();
     for (int j = tid; j < kState; j += 512) {
         uint32_t x = 0;
@@ -332,50 +335,125 @@ __global__ __launch_bounds__(512) void mt_jump_kernel(const uint32_t *src, uint3
     }
 }
 
-// One wave per chunk: words A0 + c J .. from its window, 64 elements (128 words) per step.
-__global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *wins) {
-    __shared__ uint32_t ring[1024];
-    const int c = blockIdx.x;
-    const int lane = threadIdx.x;
-    const uint32_t *win = wins + (size_t)c * kState;
-    for (int i = lane; i < kState; i += 64) ring[i] = win[i];
-    wave_lds_order();
-    const int64_t e_begin = a.eh + (int64_t)c * (kChunkWords / 2);
-    int64_t e_end = e_begin + kChunkWords / 2;
-    if (e_end > a.n) e_end = a.n;
-    // The engine block holding the last output: does it start inside this chunk's words?
+// One wave per pair of chunks, one chunk per half-wave (chunks 2 b and 2 b + 1): each half
+// makes 64 words (32 elements, one word of keep bits) per step from its chunk's window in its own
+// LDS ring.  A word depends on the word 227 before it, so a step's words depend only on steps
+// three or more back: one LDS ordering point every three steps is enough, and the three steps
+// between them overlap their LDS latency.
+struct Half {
+    int64_t e_begin;  // first element of the chunk
+    int n;            // elements of the chunk
+    int words;        // words to make: 2 n, or up to the end of the engine block it writes back
+    int sb;           // that block's first word (relative), or -1
+};
+
+DEVI Half half_of(const MtArgs &a, int c, int chunks) {
+    Half h{0, 0, 0, -1};
+    if (c >= chunks) return h;
+    h.e_begin = a.eh + (int64_t)c * (kChunkWords / 2);
+    const int64_t n = a.n - h.e_begin;
+    h.n = n < kChunkWords / 2 ? (int)n : kChunkWords / 2;
+    h.words = 2 * h.n;
     const int64_t chunk_pos = a.a0 + (int64_t)c * kChunkWords;  // relative position of word 0
-    const int64_t sb = a.state_block >= 0 ? (int64_t)a.state_block * kState - chunk_pos : -1;
-    const bool writes_state = a.state_block >= 0 && a.state_block * (int64_t)kState >= a.a0 &&
-                              sb >= 0 && sb < kChunkWords;
-    const int64_t words = writes_state && sb + kState > 2 * (e_end - e_begin)
-                              ? sb + kState : 2 * (e_end - e_begin);
-    for (int64_t base = 0; base < words; base += 128) {
-        const int u0 = (int)base + 2 * lane;
+    if (a.state_block >= 0 && a.state_block * (int64_t)kState >= a.a0) {
+        const int64_t sb = a.state_block * (int64_t)kState - chunk_pos;
+        if (sb >= 0 && sb < kChunkWords) {
+            h.sb = (int)sb;
+            if (h.sb + kState > h.words) h.words = h.sb + kState;
+        }
+    }
+    return h;
+}
+
+__global__ __launch_bounds__(64) void mt_chunk_kernel(MtArgs a, const uint32_t *wins, int chunks) {
+    __shared__ __align__(16) uint32_t rings[2][1024];
+    const int lane = threadIdx.x, half = lane >> 5, hl = lane & 31;
+    const int c = 2 * blockIdx.x + half;
+    const Half hh = half_of(a, c, chunks);
+    const int words_max = max(half_of(a, 2 * blockIdx.x, chunks).words,
+                              half_of(a, 2 * blockIdx.x + 1, chunks).words);
+    uint32_t *ring = rings[half];
+    if (c < chunks) {
+        const uint32_t *win = wins + (size_t)c * kState;
+        for (int i = hl; i < kState; i += 32) ring[i] = win[i];
+    }
+    wave_lds_order();
+    uint32_t *bits = a.bits + (hh.e_begin >> 5);  // e_begin is a multiple of 64
+    const uint64_t thr = a.thr;
+    // Keep bits of the pair (w0, w1) at words u0, u0 + 1 of this half's step starting at base.
+    auto emit = [&](int base, uint32_t w0, uint32_t w1) {
+        const int e = base / 2 + hl;
+        const uint64_t r = (((uint64_t)temper(w0) << 32) | temper(w1)) & ((1ull << 53) - 1);
+        const uint64_t m = __ballot(e < hh.n && r < thr);
+        if (hl == 0 && base / 2 < hh.n) bits[base / 64] = (uint32_t)(m >> (32 * half));
+    };
+    auto make = [&](int u0, uint32_t &w0, uint32_t &w1) {
+        const uint32_t x0 = ring[(u0 - 624) & 1023], x1 = ring[(u0 - 623) & 1023];
+        const uint32_t x2 = ring[(u0 - 622) & 1023];
+        w0 = ring[(u0 - 227) & 1023] ^ twist_d(x0, x1);
+        w1 = ring[(u0 - 226) & 1023] ^ twist_d(x1, x2);
+        *reinterpret_cast<uint2 *>(&ring[u0 & 1023]) = make_uint2(w0, w1);
+    };
+    // Words 0 .. 639: the window, then the first generated words (which read only the window).
+    for (int base = 0; base < 640; base += 64) {
+        const int u0 = base + 2 * hl;
         uint32_t w0, w1;
         if (u0 < kState) {
             w0 = ring[u0];
             w1 = ring[u0 + 1];
         } else {
-            w0 = ring[(u0 - 227) & 1023] ^ twist_d(ring[(u0 - 624) & 1023], ring[(u0 - 623) & 1023]);
-            w1 = ring[(u0 - 226) & 1023] ^ twist_d(ring[(u0 - 623) & 1023], ring[(u0 - 622) & 1023]);
-            ring[u0 & 1023] = w0;
-            ring[(u0 + 1) & 1023] = w1;
+            make(u0, w0, w1);
         }
-        const int64_t e = e_begin + base / 2 + lane;
-        const bool k = e < e_end && keep(temper(w0), temper(w1), a.thr);
-        const uint64_t m = __ballot(k);
-        const int64_t e0 = e_begin + base / 2;
-        if (e0 < e_end) {
-            if (lane == 0) a.bits[e0 >> 5] = (uint32_t)m;
-            if (lane == 1 && e0 + 32 < e_end) a.bits[(e0 >> 5) + 1] = (uint32_t)(m >> 32);
+        emit(base, w0, w1);
+    }
+    wave_lds_order();
+    bool captured = false;
+    for (int base = 640; base < words_max; base += 192) {
+        // All reads of the three steps first (none of them reads a word the three steps
+        // write), then the words, the ring writes and the keep bits.
+        uint32_t x[3][5];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int u0 = base + 64 * k + 2 * hl;
+            x[k][0] = ring[(u0 - 624) & 1023];
+            x[k][1] = ring[(u0 - 623) & 1023];
+            x[k][2] = ring[(u0 - 622) & 1023];
+            x[k][3] = ring[(u0 - 227) & 1023];
+            x[k][4] = ring[(u0 - 226) & 1023];
+        }
+        // Three independent chains, straight-line: words, ring writes, keep ballots; then the
+        // (branching) stores of the three keep words.
+        uint32_t w[3][2];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            w[k][0] = x[k][3] ^ twist_d(x[k][0], x[k][1]);
+            w[k][1] = x[k][4] ^ twist_d(x[k][1], x[k][2]);
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            *reinterpret_cast<uint2 *>(&ring[(base + 64 * k + 2 * hl) & 1023]) = make_uint2(w[k][0], w[k][1]);
+        uint64_t m[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int e = (base + 64 * k) / 2 + hl;
+            const uint64_t r = (((uint64_t)temper(w[k][0]) << 32) | temper(w[k][1])) & ((1ull << 53) - 1);
+            m[k] = __ballot(e < hh.n && r < thr);
+        }
+        if (hl == 0) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if ((base + 64 * k) / 2 < hh.n) bits[(base + 64 * k) / 64] = (uint32_t)(m[k] >> (32 * half));
         }
         wave_lds_order();
-        if (writes_state && base + 128 >= sb + kState && base < sb + kState) {
-            // Words sb .. sb + 623 are the last <= 752 words made: all still in the ring.
-            for (int i = lane; i < kState; i += 64) a.state[i] = ring[(sb + i) & 1023];
+        // The engine block this chunk writes back: copied once its last word is made (the ring
+        // still holds it: at most 624 + 191 words were made since its first).
+        if (hh.sb >= 0 && !captured && base + 192 >= hh.sb + kState) {
+            for (int i = hl; i < kState; i += 32) a.state[i] = ring[(hh.sb + i) & 1023];
+            captured = true;
         }
     }
+    if (hh.sb >= 0 && !captured)  // the block lies within words 0 .. 639
+        for (int i = hl; i < kState; i += 32) a.state[i] = ring[(hh.sb + i) & 1023];
 }
 
 // y = x * (keep ? scale : 0): the reference's input * noise, noise = bernoulli / float32(1 - p)
@@ -436,7 +514,7 @@ hipError_t launch_bernoulli(const MtArgs &a, const uint32_t *table, int chunks, 
     uint32_t *l1 = wins + kState, *l0 = l1 + (size_t)n1 * kState;
     return_if(launch(mt_jump_kernel, dim3(n1), dim3(512), st, (const uint32_t *)wins, l1, table, 1, n1));
     return_if(launch(mt_jump_kernel, dim3(chunks), dim3(512), st, (const uint32_t *)l1, l0, table, 0, chunks));
-    return launch(mt_chunk_kernel, dim3(chunks), dim3(64), st, a, (const uint32_t *)l0);
+    return launch(mt_chunk_kernel, dim3((chunks + 1) / 2), dim3(64), st, a, (const uint32_t *)l0, chunks);
 }
 
 hipError_t launch_dropout_apply(const uint32_t *bits, int64_t n, float scale, const float *x, float *y,
