@@ -85,6 +85,10 @@ dc_status launched(hipError_t e) {
     return ok();
 }
 
+// The forward's workspace: two int arrays of B*H (live key tiles per head, and the heads in
+// descending order of them), used by masks that do not depend on the query.
+size_t fwd_ws(const dc::AttnShape &s) { return round_up((size_t)2 * s.B * s.H * sizeof(int)); }
+
 size_t bwd_ws(const dc::AttnShape &s, bool bf16) {
     (void)bf16;  // both dtypes: dsum only (float32 accumulates dQ in its output)
     return round_up((size_t)s.B * s.H * s.L * sizeof(float));
@@ -166,15 +170,14 @@ int dc_abi_version(void) { return 1; }
 const char *dc_last_error(void) { return g_error.c_str(); }
 
 size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d) {
-    (void)d;
-    return 0;
+    dc::AttnShape s;
+    if (check_dims(d, &s) != DC_OK) return 0;
+    return fwd_ws(s);
 }
 
 dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
                       const float *mask, void *out, float *lse, void *workspace,
                       size_t workspace_bytes, void *stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     dc::AttnShape s;
     dc_status st = check_dims(d, &s);
     if (st != DC_OK) return st;
@@ -185,7 +188,12 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         !present(out, nq * s.E) || !present(lse, nq))
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
-    dc::FwdArgs a{s, q, k, v, out, lse};
+    dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr};
+    // A workspace too small (or none) only gives up the longest-first order of key-padding masks.
+    if (mask && workspace && workspace_bytes >= fwd_ws(s)) {
+        a.tiles = static_cast<int *>(workspace);
+        a.order = a.tiles + (size_t)s.B * s.H;
+    }
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (d->dtype == DC_F32) return launched(dc::launch_fwd_f32(a, strm));
     return launched(dc::launch_fwd_bf16(a, strm));

@@ -133,8 +133,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     const int BH = s.B * s.H;
     const int nqt = (s.L + kBM - 1) / kBM;
     const int bid = blockIdx.x;
-    const int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;  // longest causal tiles first
-    const int bh = bid % BH, b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
+    int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;  // longest causal tiles first
+    int bh = bid % BH;
+    if (ROWMASK && a.order) {
+        // Heads in descending order of live key tiles, dealt to the 8 XCDs round-robin (blocks
+        // go to XCD bid % 8), the query tiles of one head on one XCD: its K/V stays in one L2.
+        const int x = bid & 7, slot = bid >> 3;
+        const int r = 8 * (slot / nqt) + x;
+        if (r >= BH) return;
+        bh = a.order[r];
+        qt = slot % nqt;
+    }
+    const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
     const int q0 = qt * kBM;
     const int qi = q0 + wave * 32 + lr;  // this lane's query
     const int wave_last_q = q0 + wave * 32 + 31;
@@ -392,6 +402,45 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     }
 }
 
+// One wave per (b, h) of a query-independent mask: the number of BN-key tiles that hold any key
+// whose mask is not -inf (the tiles the forward computes; the others it skips).
+template <int BN>
+__global__ __launch_bounds__(64) void rowmask_tiles_kernel(FwdArgs a) {
+    static_assert(BN == 32 || BN == 64, "one or two tiles per wave-wide pass");
+    const AttnShape &s = a.s;
+    const int bh = blockIdx.x, lane = threadIdx.x;
+    const float *row = s.mask + (int64_t)(bh / s.H) * s.msb + (int64_t)(bh % s.H) * s.msh;
+    int count = 0;
+    for (int k0 = 0; k0 < s.S; k0 += 64) {
+        const int key = k0 + lane;
+        const uint64_t live = __ballot(key < s.S && row[key] != -INFINITY);
+        if (BN == 64) count += live != 0;
+        else count += ((live & 0xffffffffull) != 0) + ((live >> 32) != 0);
+    }
+    if (lane == 0) a.tiles[bh] = count;
+}
+
+// One workgroup: a counting sort of the heads by live tiles, descending (ties in any order; the
+// results do not depend on the order).
+__global__ __launch_bounds__(1024) void rowmask_order_kernel(FwdArgs a, int ntiles) {
+    __shared__ int start[kOrderMaxTiles + 1];
+    const int BH = a.s.B * a.s.H, tid = threadIdx.x;
+    for (int v = tid; v <= ntiles; v += 1024) start[v] = 0;
+    __syncthreads();
+    for (int i = tid; i < BH; i += 1024) atomicAdd(&start[a.tiles[i]], 1);
+    __syncthreads();
+    if (tid == 0) {  // start[v] = number of heads with more live tiles than v
+        int run = 0;
+        for (int v = ntiles; v >= 0; --v) {
+            const int c = start[v];
+            start[v] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < BH; i += 1024) a.order[atomicAdd(&start[a.tiles[i]], 1)] = i;
+}
+
 template <int D, int BN, int W>
 hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     FwdArgs a = args;
@@ -402,8 +451,18 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
             return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a));
-        else if (mask && a.s.msl == 0 && BN <= 64)
-            return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true, true>, grid, block, st, a));
+        else if (mask && a.s.msl == 0 && BN <= 64) {
+            const int ntiles = (a.s.S + BN - 1) / BN;
+            if (a.order && a.s.B * a.s.H <= kOrderMaxHeads && ntiles <= kOrderMaxTiles) {
+                return_if(launch(rowmask_tiles_kernel<BN>, dim3(a.s.B * a.s.H), dim3(64), st, a));
+                return_if(launch(rowmask_order_kernel, dim3(1), dim3(1024), st, a, ntiles));
+                const dim3 ogrid(nqt * 8 * ((a.s.B * a.s.H + 7) / 8));
+                return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true, true>, ogrid, block, st, a));
+            } else {
+                a.order = nullptr;
+                return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true, true>, grid, block, st, a));
+            }
+        }
         else if (mask)
             return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true>, grid, block, st, a));
         else

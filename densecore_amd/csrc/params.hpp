@@ -23,7 +23,16 @@ struct FwdArgs {
     const void *q, *k, *v;
     void *out;
     float *lse;
+    // Workspace of a query-independent mask (key padding): each (b, h)'s count of live key tiles
+    // and the (b, h) in descending order of it, which sets the workgroup order (longest first).
+    // nullptr: natural order.
+    int *tiles, *order;
 };
+
+// Longest-first ordering of a key-padding mask's heads: used when the workspace holds it and
+// the grid is small enough for one workgroup to sort.
+constexpr int kOrderMaxHeads = 65536;
+constexpr int kOrderMaxTiles = 1024;
 
 struct BwdArgs {
     AttnShape s;

@@ -64,7 +64,10 @@ typedef struct {
 /* Version of this ABI (bumped on any incompatible change). */
 int dc_abi_version(void);
 
-/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284. */
+/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  The workspace (two
+ * int arrays of batch * heads) lets a query-independent mask (mask_stride_l == 0, e.g. key
+ * padding) run its workgroups longest first; with a smaller one (or none) the forward still runs,
+ * in the natural order. */
 size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
                       const float *mask, void *out, float *lse, void *workspace,

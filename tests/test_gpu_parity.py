@@ -93,12 +93,17 @@ def test_masked_shapes(oracle_lib, B, H, L, S, E, kind):
 @pytest.mark.parametrize("B,H,L,S,E,kind", [
     (2, 3, 70, 300, 64, "padding"), (2, 2, 130, 257, 64, "holes"), (1, 4, 64, 200, 128, "holes"),
     (2, 2, 100, 100, 32, "per_head"), (1, 2, 50, 129, 48, "holes"), (2, 1, 40, 64, 64, "closed"),
+    (5, 7, 90, 333, 64, "per_bh"), (16, 16, 64, 512, 64, "padding"), (3, 11, 40, 1000, 32, "per_bh"),
 ])
 def test_row_broadcast_masks(oracle_lib, B, H, L, S, E, kind):
     """Masks that do not depend on the query (a stride-0 view along L: key padding and the like)
     take their own path in the float32 forward (one mask load per key and tile, sub-tile liveness
     from a ballot).  Padding, random holes, per-head rows, a fully masked batch row ("closed":
-    out 0, lse 0), 32-key tiles (E = 128) and the unaligned generic path (E = 48)."""
+    out 0, lse 0), 32-key tiles (E = 128) and the unaligned generic path (E = 48).  Such masks
+    also order the forward's workgroups by each head's live key tiles (longest first, a head's
+    query tiles on one XCD): per-(batch, head) prefix lengths including empty heads ("per_bh"),
+    batch * heads not a multiple of 8, and C3's 256 heads check that every (head, query tile) is
+    computed exactly once."""
     from densecore_amd import _native
     rng = np.random.default_rng(B * 7 + H * 11 + L + S + E)
     q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
@@ -110,6 +115,10 @@ def test_row_broadcast_masks(oracle_lib, B, H, L, S, E, kind):
         allowed = rng.random((B, 1, 1, S)) > 0.6
     elif kind == "per_head":
         allowed = rng.random((1, H, 1, S)) > 0.5
+    elif kind == "per_bh":
+        lens = rng.integers(0, S + 1, size=(B, H))
+        lens[0, 0], lens[-1, -1] = 0, S
+        allowed = np.arange(S)[None, None, None, :] < lens[:, :, None, None]
     else:
         allowed = np.ones((B, 1, 1, S), bool)
         allowed[0] = False
