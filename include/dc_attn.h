@@ -30,7 +30,8 @@
  * All pointers are device pointers (hipMalloc'd or equivalent).  Calls are asynchronous and
  * ordered on `stream` (a hipStream_t; NULL is the null stream).  The caller owns every buffer;
  * workspaces are sized by the matching *_workspace_size call and must be 256-byte aligned.
- * The library keeps no global mutable state except the thread-local last error.
+ * The library's only global state is the thread-local last error and, once the generator of
+ * dc_math.h is first used, its jump-ahead polynomials (built once, read-only after).
  */
 #ifndef DC_ATTN_H
 #define DC_ATTN_H
