@@ -86,8 +86,19 @@ dc_status launched(hipError_t e) {
 }
 
 // The forward's workspace: two int arrays of B*H (live key tiles per head, and the heads in
-// descending order of them), used by masks that do not depend on the query.
-size_t fwd_ws(const dc::AttnShape &s) { return round_up((size_t)2 * s.B * s.H * sizeof(int)); }
+// descending order of them), used by masks that do not depend on the query; for bf16, then the
+// scaled fp16 copy of V with its per-slab scratch (partial maxima, exponents).
+size_t fwd_order_ws(const dc::AttnShape &s) { return round_up((size_t)2 * s.B * s.H * sizeof(int)); }
+size_t fwd_v16_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * s.S * s.E * 2); }
+size_t fwd_partial_ws(const dc::AttnShape &s) {
+    return round_up((size_t)s.B * s.Hkv * dc::f16_parts((int64_t)s.S * s.E) * sizeof(float));
+}
+size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
+size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
+    size_t n = fwd_order_ws(s);
+    if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s);
+    return n;
+}
 
 size_t bwd_ws(const dc::AttnShape &s, bool bf16) {
     (void)bf16;  // both dtypes: dsum only (float32 accumulates dQ in its output)
@@ -172,7 +183,7 @@ const char *dc_last_error(void) { return g_error.c_str(); }
 size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d) {
     dc::AttnShape s;
     if (check_dims(d, &s) != DC_OK) return 0;
-    return fwd_ws(s);
+    return fwd_ws(s, d->dtype == DC_BF16);
 }
 
 dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
@@ -188,11 +199,19 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         !present(out, nq * s.E) || !present(lse, nq))
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
-    dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr};
-    // A workspace too small (or none) only gives up the longest-first order of key-padding masks.
-    if (mask && workspace && workspace_bytes >= fwd_ws(s)) {
-        a.tiles = static_cast<int *>(workspace);
+    dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
+    // A workspace too small (or none) only gives up the longest-first order of key-padding masks
+    // and, for bf16, the fp16 P V product (the bf16 hi + lo pair is used instead).
+    char *ws = static_cast<char *>(workspace);
+    if (mask && ws && workspace_bytes >= fwd_order_ws(s)) {
+        a.tiles = reinterpret_cast<int *>(ws);
         a.order = a.tiles + (size_t)s.B * s.H;
+    }
+    if (d->dtype == DC_BF16 && !mask && ws && workspace_bytes >= fwd_ws(s, true)) {
+        char *p = ws + fwd_order_ws(s);
+        a.v16 = p;
+        a.f16_partial = reinterpret_cast<float *>(p + fwd_v16_ws(s));
+        a.vexp = reinterpret_cast<int *>(p + fwd_v16_ws(s) + fwd_partial_ws(s));
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (d->dtype == DC_F32) return launched(dc::launch_fwd_f32(a, strm));

@@ -34,6 +34,19 @@ DEVI f32x16 mfma_f32(float a, float b, f32x16 c) {
 DEVI f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+// fp16 operands carried in bf16x8 registers (16-bit patterns; the tiles hold either type).
+DEVI f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                   c, 0, 0, 0);
+}
+// x[at + j] (j = 0..7) rounded to nearest fp16, as 16-bit patterns in a bf16x8 register.
+DEVI bf16x8 cvt_f16x8(const f32x16 &x, int at) {
+    f16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = static_cast<_Float16>(x[at + j]);
+    return __builtin_bit_cast(bf16x8, h);
+}
 
 // Row index (within a 32-row MFMA tile) that accumulator register r of this lane holds.
 DEVI int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }

@@ -286,7 +286,9 @@ constexpr int kPPWaves = 8;
 constexpr int kPPThreads = 64 * kPPWaves;
 constexpr int kPPM = 32 * kPPWaves;  // queries per workgroup
 
-template <int D, bool CAUSAL, bool VEC>
+// F16V: V is the fp16 copy (scaled by 2^vexp[b, kv head]) and P is rounded once to fp16, so the
+// P V product is one fp16 MFMA per fragment instead of the bf16 hi + lo pair.
+template <int D, bool CAUSAL, bool VEC, bool F16V>
 __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_pp_kernel(FwdArgs a) {
     constexpr int NT = kBN / 32, KSTEP = D / 16, NDT = D / 32;
     __shared__ KVTileBf16<D> sm[2];
@@ -368,10 +370,15 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                     bf16x8 va[NDT];
 #pragma unroll
                     for (int dt = 0; dt < NDT; ++dt) va[dt] = tr_frag<kBN, D>(vt_, trb, kt * 32 + 16 * u, dt);
+                    if constexpr (F16V) {
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], ph[kt][u], oacc[dt]);
+                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_f16(va[dt], ph[kt][u], oacc[dt]);
+                    } else {
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], pl[kt][u], oacc[dt]);
+                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], ph[kt][u], oacc[dt]);
+#pragma unroll
+                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], pl[kt][u], oacc[dt]);
+                    }
                 }
             }
         }
@@ -432,7 +439,12 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 l_part += p;
             }
 #pragma unroll
-            for (int u = 0; u < 2; ++u) split_bf16(sc[kt], 8 * u, ph[kt][u], pl[kt][u]);
+            for (int u = 0; u < 2; ++u) {
+                if constexpr (F16V)
+                    ph[kt][u] = cvt_f16x8(sc[kt], 8 * u);
+                else
+                    split_bf16(sc[kt], 8 * u, ph[kt][u], pl[kt][u]);
+            }
         }
     };
 
@@ -470,7 +482,8 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     const float l_run = xor32_add(l_part);
     if (qi < s.L) {
         const bool empty = l_run == 0.f;
-        const float inv = empty ? 0.f : 1.f / l_run;
+        float inv = empty ? 0.f : 1.f / l_run;
+        if constexpr (F16V) inv = ldexpf(inv, -a.vexp[b * s.Hkv + hk]);  // undo V's 2^vexp
         __bf16 *orow = static_cast<__bf16 *>(a.out) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
@@ -500,8 +513,16 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
     if (!mask) {
         const int nqt = (a.s.L + kPPM - 1) / kPPM;
         const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
-        if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC>, grid, block, st, a);
-        return launch(fwd_bf16_pp_kernel<D, false, VEC>, grid, block, st, a);
+        if (a.v16) {
+            FwdArgs f = a;
+            return_if(launch_to_f16(a.v, a.v16, (int64_t)a.s.B * a.s.Hkv, (int64_t)a.s.S * a.s.E,
+                                    a.f16_partial, a.vexp, st));
+            f.v = a.v16;
+            if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, true>, grid, block, st, f);
+            return launch(fwd_bf16_pp_kernel<D, false, VEC, true>, grid, block, st, f);
+        }
+        if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, false>, grid, block, st, a);
+        return launch(fwd_bf16_pp_kernel<D, false, VEC, false>, grid, block, st, a);
     }
     const int nqt = (a.s.L + kBM - 1) / kBM;
     const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);

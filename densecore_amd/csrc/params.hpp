@@ -27,6 +27,11 @@ struct FwdArgs {
     // and the (b, h) in descending order of it, which sets the workgroup order (longest first).
     // nullptr: natural order.
     int *tiles, *order;
+    // bf16 inputs: V copied to fp16, scaled by 2^vexp per (b, kv head) (f16_stage.hip), with the
+    // copy's scratch; nullptr: P enters the P V product as bf16 hi + lo.
+    void *v16;
+    float *f16_partial;
+    int *vexp;
 };
 
 // Longest-first ordering of a key-padding mask's heads: used when the workspace holds it and
@@ -63,6 +68,11 @@ struct SoftmaxArgs {
     int64_t msb, msh, msl;
     bool safe;
 };
+
+// bf16 -> fp16 copies scaled per slab (f16_stage.hip): segments per slab, and the two passes.
+int f16_parts(int64_t slab);
+hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t slab, float *partial, int *exps,
+                         hipStream_t st);
 
 // Each launcher returns hipSuccess or the launch error; it never synchronizes.
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st);

@@ -210,3 +210,26 @@ def test_bf16_backward_bit_reproducible():
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv"), first, second):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("vscale_log2", [-100, 0, 20, 100])
+def test_bf16_value_scales(oracle_lib, vscale_log2):
+    """The forward's P V product runs on an fp16 copy of V scaled per (batch, kv head) by a power
+    of two: values of magnitude 2^+-100 (far outside fp16's range) and per-head scales that differ
+    by 2^20 must come out as exactly as N(0, 1) values do."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(vscale_log2 + 500)
+    B, H, L, E = 2, 3, 150, 64
+    q = bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32))
+    k = bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32))
+    v = bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32))
+    v *= np.float32(2.0 ** vscale_log2)
+    v[1, 2] *= np.float32(2.0 ** -20)  # a head 2^20 smaller than the others
+    print(f"[case] bf16 V scale 2^{vscale_log2}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    out, lse = _native._flash_attention(_bf(q), _bf(k), _bf(v), True)
+    got = _np(out)
+    for b in range(B):
+        for h in range(H):
+            assert_bf16(got[b, h], ref_o[b, h], f"out b{b} h{h}")
+    assert_bf16(_np(lse), ref_l, "lse")
