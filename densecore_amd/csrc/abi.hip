@@ -5,6 +5,7 @@
 // attention_mask, :658-663 backward shapes); violations return DC_INVALID_ARGUMENT with the
 // reference's ValueError text.  Launch failures return DC_EXECUTION_FAILED (the reference's
 // RuntimeError, src/lib.rs:633, 677).
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <string>
@@ -100,10 +101,37 @@ size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
     return n;
 }
 
-size_t bwd_ws(const dc::AttnShape &s, bool bf16) {
-    (void)bf16;  // both dtypes: dsum only (float32 accumulates dQ in its output)
-    return round_up((size_t)s.B * s.H * s.L * sizeof(float));
+// The backward's workspace: dsum (B*H*L floats; float32 accumulates dQ in its output), then for
+// bf16 the scaled fp16 copies of q, k, v, dout with their per-slab scratch.
+struct BwdLayout {
+    size_t dsum, q16, k16, v16, do16, partial, exps, total;
+};
+BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
+    BwdLayout l{};
+    size_t at = 0;
+    auto take = [&](size_t n) {
+        const size_t off = at;
+        at += round_up(n);
+        return off;
+    };
+    l.dsum = take((size_t)s.B * s.H * s.L * sizeof(float));
+    if (bf16) {
+        const size_t nq = (size_t)s.B * s.H * s.L * s.E, nk = (size_t)s.B * s.Hkv * s.S * s.E;
+        const int64_t qslab = (int64_t)s.repeat * s.L * s.E, kslab = (int64_t)s.S * s.E;
+        const int parts = std::max(dc::f16_parts(qslab), dc::f16_parts(kslab));
+        l.q16 = take(nq * 2);
+        l.do16 = take(nq * 2);
+        l.k16 = take(nk * 2);
+        l.v16 = take(nk * 2);
+        l.partial = take((size_t)s.B * s.Hkv * parts * sizeof(float));
+        l.exps = take((size_t)4 * s.B * s.Hkv * sizeof(int));
+    }
+    l.total = at;
+    return l;
 }
+size_t bwd_ws(const dc::AttnShape &s, bool bf16) { return bwd_layout(s, bf16).total; }
+// The least the backward needs (dsum): the bf16 fp16 copies are used only when they fit.
+size_t bwd_ws_min(const dc::AttnShape &s) { return bwd_layout(s, false).total; }
 
 size_t decode_ws(const dc::AttnShape &s) {
     int split_len = 0;
@@ -233,13 +261,13 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     if (st != DC_OK) return st;
     if ((st = check_mask(d, mask, &s)) != DC_OK) return st;
     const bool bf16 = d->dtype == DC_BF16;
-    if (workspace_bytes < bwd_ws(s, bf16))
+    if (workspace_bytes < bwd_ws_min(s))
         return fail(DC_INVALID_ARGUMENT, "flash attention backward workspace is too small");
     const int64_t nq = (int64_t)s.B * s.H * s.L, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
     if (!present(grad_out, nq * s.E) || !present(q, nq * s.E) || !present(k, nkv) ||
         !present(v, nkv) || !present(out, nq * s.E) || !present(lse, nq) ||
         !present(dq, nq * s.E) || !present(dk, nkv) || !present(dv, nkv) ||
-        !present(workspace, (int64_t)bwd_ws(s, bf16)))
+        !present(workspace, (int64_t)bwd_ws_min(s)))
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     if (nq == 0 && nkv == 0) return ok();
     s.vec = aligned16(grad_out) && aligned16(q) && aligned16(k) && aligned16(v) &&
@@ -251,6 +279,13 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     a.dq = dq, a.dk = dk, a.dv = dv;
     a.dsum = reinterpret_cast<float *>(ws);
     a.dq_acc = bf16 ? nullptr : static_cast<float *>(dq);
+    // bf16: the fp16 products when the workspace holds the copies (else the bf16 hi + lo pairs).
+    if (bf16 && workspace_bytes >= bwd_ws(s, true)) {
+        const BwdLayout l = bwd_layout(s, true);
+        a.q16 = ws + l.q16, a.k16 = ws + l.k16, a.v16 = ws + l.v16, a.do16 = ws + l.do16;
+        a.f16_partial = reinterpret_cast<float *>(ws + l.partial);
+        a.exps = reinterpret_cast<int *>(ws + l.exps);
+    }
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
     return launched(dc::launch_bwd_bf16(a, strm));

@@ -68,7 +68,37 @@ struct alignas(16) DkdvSmem {
     };
 };
 
-template <int D, bool CAUSAL, bool MASK, bool VEC>
+// The fp16 mode of both kernels (F16): q, k, v, dout are the fp16 copies, scaled by 2^e_q,
+// 2^e_k, 2^e_v, 2^e_do per (b, kv head), and P and dS are rounded once to fp16, so each of the
+// P / dS products is one fp16 MFMA instead of the bf16 hi + lo pair.  The scores' scale takes
+// 2^-(e_q + e_k), dsum is stored times 2^(e_do + e_v) so that dP - dsum comes out scaled by
+// that too, and dS is formed as P (dP - dsum) 2^(e_do + e_v - 24): |dP - dsum| is below
+// 2 E max|dO| max|V| (dsum = dO . out with |out| <= max|V|), so this is below 2^14 for E <= 128.
+// The outputs take the inverse powers: dV 2^-e_do, dK 2^-(e_q + e_do + e_v - 24), dQ
+// 2^-(e_k + e_do + e_v - 24).
+struct F16Scales {
+    float sc_log2 = 0.f, sc = 0.f;  // scale (base 2 and natural), times 2^-(e_q + e_k)
+    int e_pv = 0;                   // e_do + e_v
+    int e_q = 0, e_k = 0, e_do = 0;
+};
+
+DEVI F16Scales f16_scales(const BwdArgs &a, int bhk) {
+    const int n = a.s.B * a.s.Hkv;
+    F16Scales f;
+    f.e_q = a.exps[bhk], f.e_k = a.exps[n + bhk], f.e_do = a.exps[3 * n + bhk];
+    f.e_pv = f.e_do + a.exps[2 * n + bhk];
+    f.sc_log2 = ldexpf(a.s.scale_log2, -(f.e_q + f.e_k));
+    f.sc = ldexpf(a.s.scale, -(f.e_q + f.e_k));
+    return f;
+}
+
+template <bool F16>
+DEVI f32x16 mfma16(bf16x8 x, bf16x8 y, f32x16 c) {
+    if constexpr (F16) return mfma_f16(x, y, c);
+    else return mfma_bf16(x, y, c);
+}
+
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16>
 __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32;
     __shared__ DkdvSmem<D> sm;
@@ -86,6 +116,9 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)bhk * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)bhk * s.S * s.E;
+    F16Scales fs;
+    if constexpr (F16) fs = f16_scales(a, bhk);
+    const float sc_log2 = F16 ? fs.sc_log2 : s.scale_log2, sc = F16 ? fs.sc : s.scale;
     const int nkeys = min(kKN, s.S - n0);
     fill_cm<kKN, D, VEC, kKW>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
     fill_cm<kKN, D, VEC, kKW>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
@@ -108,7 +141,8 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     auto load_row_stat = [&](int i) -> float {
         const int bh = step_bh(i), qq = step_m0(i) + lane;
         if (wave == 0) return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e : -INFINITY;
-        return qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
+        const float ds = qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
+        return F16 ? ldexpf(ds, fs.e_pv) : ds;
     };
     auto store_row_stat = [&](int i, float x) {
         if (wave == 0) sm.m.lse[i & 1][lane] = x;
@@ -149,10 +183,10 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
             for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
 #pragma unroll
             for (int st = 0; st < KSTEP; ++st) {
-                sacc = mfma_bf16(row_frag<kKM, D>(qt, rowb, 32 * qh, st),
-                                 row_frag<kKN, D>(sm.m.k, rowbk, 32 * kw, st), sacc);
-                pacc = mfma_bf16(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
-                                 row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
+                sacc = mfma16<F16>(row_frag<kKM, D>(qt, rowb, 32 * qh, st),
+                                   row_frag<kKN, D>(sm.m.k, rowbk, 32 * kw, st), sacc);
+                pacc = mfma16<F16>(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
+                                   row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
             }
             // Keep the operand reads (two per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 2, 4>();
@@ -172,14 +206,14 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                         float x;
                         if (MASK) {
                             const float mk = (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-                            x = fmaf(fmaf(sacc[r], s.scale, mk), kLog2e, nl[j]);
+                            x = fmaf(fmaf(sacc[r], sc, mk), kLog2e, nl[j]);
                         } else {
-                            x = fmaf(sacc[r], s.scale_log2, nl[j]);
+                            x = fmaf(sacc[r], sc_log2, nl[j]);
                         }
                         if (EDGE && (key >= s.S || (CAUSAL && key > qq))) x = -INFINITY;
                         const float p = exp2_fast(x);
                         sacc[r] = p;
-                        pacc[r] = p * (pacc[r] - dsm[j]);
+                        pacc[r] = F16 ? p * (pacc[r] - dsm[j]) * 0x1p-24f : p * (pacc[r] - dsm[j]);
                     }
                 }
             };
@@ -191,21 +225,27 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
             for (int u = 0; u < 2; ++u) {
                 const int row0 = 32 * qh + 16 * u;
                 bf16x8 ph, pl;
-                split_bf16(sacc, 8 * u, ph, pl);
+                if constexpr (F16) ph = cvt_f16x8(sacc, 8 * u);
+                else split_bf16(sacc, 8 * u, ph, pl);
                 bf16x8 fa[NDT];
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(ot, trb, row0, dt);
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], ph, dv[dt]);
+                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma16<F16>(fa[dt], ph, dv[dt]);
+                if constexpr (!F16) {
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], pl, dv[dt]);
-                split_bf16(pacc, 8 * u, ph, pl);
+                    for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], pl, dv[dt]);
+                }
+                if constexpr (F16) ph = cvt_f16x8(pacc, 8 * u);
+                else split_bf16(pacc, 8 * u, ph, pl);
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(qt, trb, row0, dt);
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], ph, dk[dt]);
+                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma16<F16>(fa[dt], ph, dk[dt]);
+                if constexpr (!F16) {
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], pl, dk[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], pl, dk[dt]);
+                }
             }
         }
         if (i + 1 < nsteps && wave < 2) store_row_stat(i + 1, stat);
@@ -233,6 +273,10 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         for (int r = 0; r < 16; ++r) {
             dk[dt][r] += sm.r.acc[kw][dt][r][lane];
             dv[dt][r] += sm.r.acc[kw][NDT + dt][r][lane];
+            if constexpr (F16) {  // undo the copies' scales (exact powers of two)
+                dk[dt][r] = ldexpf(dk[dt][r], -(fs.e_q + fs.e_pv - 24));
+                dv[dt][r] = ldexpf(dv[dt][r], -fs.e_do);
+            }
         }
     __bf16 *dkr = static_cast<__bf16 *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
     __bf16 *dvr = static_cast<__bf16 *>(a.dv) + ((int64_t)bhk * s.S + key) * s.E;
@@ -276,7 +320,7 @@ struct alignas(16) DqSmem {
     u32x4 v[2][T::SLOTS];
 };
 
-template <int D, bool CAUSAL, bool MASK, bool VEC>
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32, NT = kQN / 32;
     __shared__ DqSmem<D> sm;
@@ -294,6 +338,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
+    F16Scales fs;
+    if constexpr (F16) fs = f16_scales(a, b * s.Hkv + hk);
+    const float sc_log2 = F16 ? fs.sc_log2 : s.scale_log2, sc = F16 ? fs.sc : s.scale;
 
     // Q and dO rows of this lane's query as B operands (step t, half g: dims 16t + 8g + 0..7).
     bf16x8 qreg[KSTEP], oreg[KSTEP];
@@ -321,7 +368,8 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     // -lse in base 2.  (The float32 kernels subtract lse in natural-log units first, which
     // saves one rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
     const float nlse2 = -lse_q * kLog2e;
-    const float dsum_q = qi < s.L ? a.dsum[(int64_t)bh * s.L + qi] : 0.f;
+    float dsum_q = qi < s.L ? a.dsum[(int64_t)bh * s.L + qi] : 0.f;
+    if constexpr (F16) dsum_q = ldexpf(dsum_q, fs.e_pv);
     const float *mrow = nullptr;
     if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
 
@@ -377,8 +425,8 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
 #pragma unroll
             for (int st = 0; st < KSTEP; ++st) {
-                sacc = mfma_bf16(row_frag<kQN, D>(kt_, rowb, 32 * kt, st), qreg[st], sacc);
-                pacc = mfma_bf16(row_frag<kQN, D>(vt_, rowb, 32 * kt, st), oreg[st], pacc);
+                sacc = mfma16<F16>(row_frag<kQN, D>(kt_, rowb, 32 * kt, st), qreg[st], sacc);
+                pacc = mfma16<F16>(row_frag<kQN, D>(vt_, rowb, 32 * kt, st), oreg[st], pacc);
             }
             // Keep the operand reads (one per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 1, 4>();
@@ -390,13 +438,14 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                 for (int r = 0; r < 16; ++r) {
                     // exponent in base 2: scale q.k (+ mask) - lse, times log2 e
                     float x;
-                    if (MASK) x = fmaf(fmaf(sacc[r], s.scale, mv[kt][r]), kLog2e, nlse2);
-                    else x = fmaf(sacc[r], s.scale_log2, nlse2);
+                    if (MASK) x = fmaf(fmaf(sacc[r], sc, mv[kt][r]), kLog2e, nlse2);
+                    else x = fmaf(sacc[r], sc_log2, nlse2);
                     if (EDGE) {
                         const int key = n0 + kt * 32 + acc_row(r, g);
                         if (key >= s.S || (CAUSAL && key > qi)) x = -INFINITY;
                     }
-                    sacc[r] = exp2_fast(x) * (pacc[r] - dsum_q);
+                    sacc[r] = F16 ? exp2_fast(x) * (pacc[r] - dsum_q) * 0x1p-24f
+                                  : exp2_fast(x) * (pacc[r] - dsum_q);
                 }
             };
             if (edge) elementwise(std::true_type{});
@@ -405,18 +454,27 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 bf16x8 sh, sl;
-                split_bf16(sacc, 8 * u, sh, sl);
+                if constexpr (F16) sh = cvt_f16x8(sacc, 8 * u);
+                else split_bf16(sacc, 8 * u, sh, sl);
                 bf16x8 fa[NDT];
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kQN, D>(kt_, trb, 32 * kt + 16 * u, dt);
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sh, dq[dt]);
+                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[dt], sh, dq[dt]);
+                if constexpr (!F16) {
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sl, dq[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sl, dq[dt]);
+                }
             }
         }
     }
 
+    if constexpr (F16) {  // undo the copies' scales (exact powers of two)
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dq[dt][r] = ldexpf(dq[dt][r], -(fs.e_k + fs.e_pv - 24));
+    }
     if (qi < s.L) {
         __bf16 *dqr = static_cast<__bf16 *>(a.dq) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
@@ -439,24 +497,40 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
 }
 
-template <int D, bool VEC>
-hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
+template <int D, bool VEC, bool F16>
+hipError_t launch_dvf(const BwdArgs &a, hipStream_t st) {
     const bool mask = a.s.mask != nullptr, causal = a.s.causal;
     const dim3 gk(((a.s.S + kKN - 1) / kKN) * a.s.B * a.s.Hkv), bk(kKThreads);
     const dim3 gq(((a.s.L + kQM - 1) / kQM) * a.s.B * a.s.H), bq(kQThreads);
     if (a.s.S > 0) {
-        if (causal && mask) return_if(launch(bwd_dkdv_bf16_kernel<D, true, true, VEC>, gk, bk, st, a));
-        else if (causal) return_if(launch(bwd_dkdv_bf16_kernel<D, true, false, VEC>, gk, bk, st, a));
-        else if (mask) return_if(launch(bwd_dkdv_bf16_kernel<D, false, true, VEC>, gk, bk, st, a));
-        else return_if(launch(bwd_dkdv_bf16_kernel<D, false, false, VEC>, gk, bk, st, a));
+        if (causal && mask) return_if(launch(bwd_dkdv_bf16_kernel<D, true, true, VEC, F16>, gk, bk, st, a));
+        else if (causal) return_if(launch(bwd_dkdv_bf16_kernel<D, true, false, VEC, F16>, gk, bk, st, a));
+        else if (mask) return_if(launch(bwd_dkdv_bf16_kernel<D, false, true, VEC, F16>, gk, bk, st, a));
+        else return_if(launch(bwd_dkdv_bf16_kernel<D, false, false, VEC, F16>, gk, bk, st, a));
     }
     if (a.s.L > 0) {
-        if (causal && mask) return_if(launch(bwd_dq_bf16_kernel<D, true, true, VEC>, gq, bq, st, a));
-        else if (causal) return_if(launch(bwd_dq_bf16_kernel<D, true, false, VEC>, gq, bq, st, a));
-        else if (mask) return_if(launch(bwd_dq_bf16_kernel<D, false, true, VEC>, gq, bq, st, a));
-        else return_if(launch(bwd_dq_bf16_kernel<D, false, false, VEC>, gq, bq, st, a));
+        if (causal && mask) return_if(launch(bwd_dq_bf16_kernel<D, true, true, VEC, F16>, gq, bq, st, a));
+        else if (causal) return_if(launch(bwd_dq_bf16_kernel<D, true, false, VEC, F16>, gq, bq, st, a));
+        else if (mask) return_if(launch(bwd_dq_bf16_kernel<D, false, true, VEC, F16>, gq, bq, st, a));
+        else return_if(launch(bwd_dq_bf16_kernel<D, false, false, VEC, F16>, gq, bq, st, a));
     }
     return hipSuccess;
+}
+
+// With the fp16 copies: convert (q and dout per group of query heads sharing a kv head, k and
+// v per kv head), then run the kernels on the copies.
+template <int D, bool VEC>
+hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
+    if (!a.q16) return launch_dvf<D, VEC, false>(a, st);
+    const int64_t n = (int64_t)a.s.B * a.s.Hkv;
+    const int64_t qslab = (int64_t)a.s.repeat * a.s.L * a.s.E, kslab = (int64_t)a.s.S * a.s.E;
+    return_if(launch_to_f16(a.q, a.q16, n, qslab, a.f16_partial, a.exps, st));
+    return_if(launch_to_f16(a.k, a.k16, n, kslab, a.f16_partial, a.exps + n, st));
+    return_if(launch_to_f16(a.v, a.v16, n, kslab, a.f16_partial, a.exps + 2 * n, st));
+    return_if(launch_to_f16(a.dout, a.do16, n, qslab, a.f16_partial, a.exps + 3 * n, st));
+    BwdArgs f = a;
+    f.q = a.q16, f.k = a.k16, f.v = a.v16, f.dout = a.do16;
+    return launch_dvf<D, VEC, true>(f, st);
 }
 
 template <int D>

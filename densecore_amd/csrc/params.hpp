@@ -46,6 +46,12 @@ struct BwdArgs {
     void *dq, *dk, *dv;
     float *dsum;    // (B, H, L) workspace: rowsum(dout * out)
     float *dq_acc;  // (B, H, L, E) float32 accumulator (== dq for float32)
+    // bf16: q, k, v, dout copied to fp16 (f16_stage.hip), each scaled by 2^e per (b, kv head)
+    // (q and dout per group of query heads sharing a kv head); exps holds e_q, e_k, e_v, e_do,
+    // B*Hkv each.  nullptr: P and dS enter their products as bf16 hi + lo.
+    void *q16, *k16, *v16, *do16;
+    float *f16_partial;
+    int *exps;
 };
 
 struct DecodeArgs {
