@@ -65,17 +65,20 @@ typedef struct {
 /* Version of this ABI (bumped on any incompatible change). */
 int dc_abi_version(void);
 
-/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  The workspace (two
- * int arrays of batch * heads) lets a query-independent mask (mask_stride_l == 0, e.g. key
- * padding) run its workgroups longest first; with a smaller one (or none) the forward still runs,
- * in the natural order. */
+/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  The workspace is
+ * optional: it holds the longest-first workgroup order of a query-independent mask
+ * (mask_stride_l == 0, e.g. key padding) and, for bf16 without a mask, the power-of-two-scaled
+ * fp16 copy of v that the P V product uses.  With less (or none) the forward runs in the natural
+ * order and, for bf16, takes P as a bf16 hi + lo pair. */
 size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
                       const float *mask, void *out, float *lse, void *workspace,
                       size_t workspace_bytes, void *stream);
 
 /* Backward (dq, dk, dv) from the saved out and lse.  src/lib.rs:640-683,
- * src/torch_attention.rs:286-468. */
+ * src/torch_attention.rs:286-468.  The workspace must hold dsum (batch * heads * q_len floats);
+ * the size returned also covers, for bf16, scaled fp16 copies of q, k, v and grad_out (with
+ * less, P and dS enter their products as bf16 hi + lo pairs). */
 size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q, const void *k,
                       const void *v, const void *out, const float *lse, const float *mask,

@@ -144,8 +144,14 @@ def test_mask_strides_and_workspace_checks():
     st = L.dc_sdpa_bwd(ctypes.byref(d), *([None] * 11), need - 1, None)
     assert st == _lib.DC_INVALID_ARGUMENT and "workspace" in L.dc_last_error().decode()
     bf = desc(dtype=_lib.DC_BF16)
-    # bf16 needs only dsum too: its dQ kernel writes dq directly (no float32 accumulator)
-    assert L.dc_sdpa_bwd_workspace_size(ctypes.byref(bf)) == need
+    # bf16 asks for dsum plus the fp16 copies of q, k, v, dout (B2 H4 L8 E16: 2 x 1024 + 2 x 512
+    # halves) and their scratch; with only dsum it still runs (the bf16 hi + lo products).
+    need_bf = L.dc_sdpa_bwd_workspace_size(ctypes.byref(bf))
+    assert need_bf >= need + 2 * (2 * 4 * 8 * 16) * 2 + 2 * (2 * 2 * 8 * 16) * 2
+    st = L.dc_sdpa_bwd(ctypes.byref(bf), *([None] * 11), need - 1, None)
+    assert st == _lib.DC_INVALID_ARGUMENT and "workspace" in L.dc_last_error().decode()
+    fw = L.dc_sdpa_fwd_workspace_size(ctypes.byref(bf))
+    assert fw >= L.dc_sdpa_fwd_workspace_size(ctypes.byref(d)) + 2 * 2 * 8 * 16 * 2  # + V's fp16 copy
     dd = desc(q_len=2)
     st = L.dc_sdpa_decode(ctypes.byref(dd), *([None] * 6), 1 << 20, None)
     assert st == _lib.DC_INVALID_ARGUMENT and "q_len == 1" in L.dc_last_error().decode()

@@ -233,3 +233,33 @@ def test_bf16_value_scales(oracle_lib, vscale_log2):
         for h in range(H):
             assert_bf16(got[b, h], ref_o[b, h], f"out b{b} h{h}")
     assert_bf16(_np(lse), ref_l, "lse")
+
+
+def test_bf16_without_fp16_copies(oracle_lib):
+    """A caller that passes no forward workspace and only dsum for the backward gets the bf16
+    hi + lo products (no fp16 copies): the same bar on the same shape."""
+    import ctypes
+    from densecore_amd import _lib, _native
+    rng = np.random.default_rng(77)
+    B, H, L, E = 1, 4, 300, 128
+    q, k, v, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(4))
+    print("[case] bf16 minimal workspaces", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, True)
+    tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
+    out = torch.empty_like(tq)
+    lse = torch.empty((B, H, L), dtype=torch.float32, device=DEV)
+    d = _native._desc((B, H, H, L, L, E), True, None, torch.bfloat16, (0, 0, 0))
+    Lb = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(Lb.dc_sdpa_fwd(d, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), None, out.data_ptr(),
+                              lse.data_ptr(), None, 0, stream))
+    assert_bf16(_np(out), ref_o, "out")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), True)
+    dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
+    ws = torch.empty(B * H * L * 4 + 256, dtype=torch.uint8, device=DEV)
+    assert ws.numel() < Lb.dc_sdpa_bwd_workspace_size(d)
+    _lib.check(Lb.dc_sdpa_bwd(d, tg.data_ptr(), tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), out.data_ptr(),
+                              lse.data_ptr(), None, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                              ws.data_ptr(), ws.numel(), stream))
+    for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        assert_bf16(_np(a), r, name)
