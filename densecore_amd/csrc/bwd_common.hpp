@@ -8,11 +8,12 @@ namespace dc {
 
 // dsum[row] = sum_d dO[row][d] * O[row][d]; with CLEAR also zeroes the float32 dQ accumulator
 // row (the float32 backward accumulates dQ into its output with atomics).
+// One 256-thread block handles rows 16 * block .. 16 * block + 15.
 template <typename T, bool CLEAR>
-__global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
+DEVI void bwd_pre_block(const BwdArgs &a, int64_t block) {
     const AttnShape &s = a.s;
     const int64_t rows = (int64_t)s.B * s.H * s.L;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t row = block * 16 + (threadIdx.x >> 4);
     const int part = threadIdx.x & 15;
     if (row >= rows) return;  // whole 16-lane groups exit together
     const T *go = static_cast<const T *>(a.dout) + row * s.E;
@@ -26,6 +27,11 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
         float *dq = a.dq_acc + row * s.E;
         for (int d = part; d < s.E; d += 16) dq[d] = 0.f;
     }
+}
+
+template <typename T, bool CLEAR>
+__global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
+    bwd_pre_block<T, CLEAR>(a, blockIdx.x);
 }
 
 }  // namespace dc

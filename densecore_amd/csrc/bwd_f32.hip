@@ -18,6 +18,11 @@
 //     accumulator with one coalesced global atomic per element and workgroup step.  That
 //     product runs between the next step's two barriers, so it costs no barrier of its own.
 // A small pre-kernel computes dsum and clears the dQ accumulator.
+//
+// When whole key tiles would leave part of the device idle (fewer tiles than workgroups that fit
+// at once, or a ragged last wave of equal non-causal tiles), a stream-K schedule replaces the
+// one-workgroup-per-tile grid: as many workgroups as fit at once each take an equal range of
+// the steps of all tiles, and tiles cut between ranges add their dK / dV atomically.
 #include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
@@ -157,18 +162,40 @@ DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L,
     }
 }
 
+// Query steps of key tile kt (keys kt * kBN ..): (query head of the kv head, 32-query tile)
+// pairs, query head outermost; causal skips the query tiles that end before the tile's first key
+// (kBN is a multiple of kBM, so the first step starts at that key).
+__host__ __device__ inline int tile_m_begin(bool causal, int kt) { return causal ? kt * kBN : 0; }
+__host__ __device__ inline int tile_per_head(const AttnShape &s, int kt) {
+    const int m_begin = tile_m_begin(s.causal, kt);
+    return s.L > m_begin ? (s.L - m_begin + kBM - 1) / kBM : 0;
+}
+__host__ __device__ inline int tile_steps(const AttnShape &s, int kt) { return tile_per_head(s, kt) * s.repeat; }
+
+// Stream-K schedule: the steps of all key tiles, in (batch * kv head, key tile, step) order, cut
+// into `chunks` equal ranges, one per workgroup.  A key tile whose steps fall in more than one
+// range is "split": its workgroups add their dK / dV into outputs the pre-kernel cleared.
+struct StreamK {
+    int64_t total;    // steps of all key tiles
+    int64_t per_kvh;  // steps of one (batch, kv head)
+    int chunks;       // a multiple of 8
+};
+
+// The range holding step p: the largest c with floor(c * total / chunks) <= p.
+__host__ __device__ inline int64_t chunk_of(const StreamK &k, int64_t p) {
+    return ((p + 1) * k.chunks - 1) / k.total;
+}
+
+// Steps [i0, i1) of key tile kt of (batch, kv head) bhk, by one workgroup; `whole`: these are all
+// of the tile's steps, so dK / dV are stored, else added atomically.
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
+DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, bool whole) {
     constexpr int DH = D / 2;
     constexpr int NDT = D / 32;
-    __shared__ BwdSmem<D> sm;
 
     const AttnShape &s = a.s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
-    const int BHk = s.B * s.Hkv;
-    const int bid = blockIdx.x;
-    const int kt = bid / BHk;  // kv tile; tile 0 has the most causal work, so it goes first
-    const int bhk = bid % BHk, b = bhk / s.Hkv, hk = bhk % s.Hkv;
+    const int wave = tid >> 6, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int b = bhk / s.Hkv, hk = bhk % s.Hkv;
     const int n0 = kt * kBN;
     const int kw0 = n0 + wave * 32;  // this wave's first key
     const int key = kw0 + lr;        // this lane's key column
@@ -221,11 +248,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[dt][r] = 0.f, dv[dt][r] = 0.f;
 
-    // Steps run over (query head of this kv head, 32-query tile); causal skips the tiles
-    // that end before this workgroup's first key.
-    const int m_begin = CAUSAL ? (n0 / kBM) * kBM : 0;
-    const int per_head = s.L > m_begin ? (s.L - m_begin + kBM - 1) / kBM : 0;
-    const int nsteps = per_head * s.repeat;
+    const int m_begin = tile_m_begin(CAUSAL, kt);
+    const int per_head = tile_per_head(s, kt);
     const int key_end = min(kBN, s.S - n0);  // keys of this tile that exist
     auto step_head = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
     auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kBM; };
@@ -233,14 +257,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
 
     QStage<D> stage;
-    if (VEC && nsteps > 0) {
-        const int bh = step_head(0);
+    if (VEC && i0 < i1) {
+        const int bh = step_head(i0);
         stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
                    static_cast<const float *>(a.dout) + (int64_t)bh * s.L * D,
-                   a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, step_m0(0), s.L, tid);
+                   a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, step_m0(i0), s.L, tid);
     }
     int prev_bh = -1, prev_m0 = 0;
-    for (int i = 0; i < nsteps; ++i) {
+    for (int i = i0; i < i1; ++i) {
         const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
         __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
         if (prev_bh >= 0)
@@ -254,7 +278,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
                              a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
         }
         __syncthreads();  // the tile is staged and the previous dQ product has read sm.ds
-        if (VEC && i + 1 < nsteps) {
+        if (VEC && i + 1 < i1) {
             const int nbh = step_head(i + 1);
             stage.load(static_cast<const float *>(a.q) + (int64_t)nbh * s.L * D,
                        static_cast<const float *>(a.dout) + (int64_t)nbh * s.L * D,
@@ -319,6 +343,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0), s.L,
                       s.E, s.scale, wave, lane);
 
+    if (!whole) {
+        // A share of the tile's steps: dK and dV are added atomically.  Each wave's 32 x D block
+        // goes through LDS first (the whole shared area is free after the last dQ product), so
+        // that one atomic instruction covers consecutive dims of one key: straight from the
+        // accumulators (one key per lane) it would touch 64 cache lines.
+        constexpr int RS = D + 4;  // padded rows: the 16-byte writes of 8 keys hit distinct banks
+        static_assert(4 * 32 * RS * sizeof(float) <= sizeof(BwdSmem<D>), "per-wave blocks fit");
+        float *blk = reinterpret_cast<float *>(&sm) + wave * 32 * RS;
+        const int rows = min(32, s.S - kw0);
+        auto flush = [&](const f32x16 (&acc)[NDT], float mul, float *dst) {
+            __syncthreads();  // the previous readers of the area are done
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; r += 4)
+                    *reinterpret_cast<f32x4 *>(blk + lr * RS + dt * 32 + acc_row(r, g)) =
+                        f32x4{acc[dt][r] * mul, acc[dt][r + 1] * mul, acc[dt][r + 2] * mul,
+                              acc[dt][r + 3] * mul};
+            __syncthreads();
+            for (int i = lane; i < rows * D; i += 64) {
+                const int rr = i / D, d = i % D;
+                if (d < s.E) unsafeAtomicAdd(dst + (int64_t)rr * s.E + d, blk[rr * RS + d]);
+            }
+        };
+        flush(dk, s.scale, static_cast<float *>(a.dk) + ((int64_t)bhk * s.S + kw0) * s.E);
+        flush(dv, 1.f, static_cast<float *>(a.dv) + ((int64_t)bhk * s.S + kw0) * s.E);
+        return;
+    }
+
     // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
     if (key < s.S) {
         float *dkr = static_cast<float *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
@@ -346,11 +399,118 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     }
 }
 
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
+    __shared__ BwdSmem<D> sm;
+    const int BHk = a.s.B * a.s.Hkv;
+    const int kt = blockIdx.x / BHk;  // tile 0 has the most causal work, so it goes first
+    key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, blockIdx.x % BHk, kt, 0, tile_steps(a.s, kt), true);
+}
+
+// One workgroup per range of the stream-K schedule, ranges dealt to the 8 XCDs in contiguous
+// blocks (workgroup w runs on XCD w % 8), so the key tiles of one kv head, which read the same
+// Q / dO, share an L2.
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
+    __shared__ BwdSmem<D> sm;
+    const int w = blockIdx.x;
+    const int64_t c = (int64_t)(w & 7) * (sk.chunks >> 3) + (w >> 3);
+    int64_t pos = c * sk.total / sk.chunks;
+    const int64_t end = (c + 1) * sk.total / sk.chunks;
+    const int nkt = (a.s.S + kBN - 1) / kBN;
+    // The key tile and step of the first position (tiles without steps hold no position).
+    int bhk = (int)(pos / sk.per_kvh), kt = 0;
+    int64_t r = pos % sk.per_kvh;
+    for (; kt < nkt; ++kt) {
+        const int n = tile_steps(a.s, kt);
+        if (r < n) break;
+        r -= n;
+    }
+    int i = (int)r;
+    bool first = true;
+    while (pos < end) {
+        const int n = tile_steps(a.s, kt);
+        const int i1 = (int)min((int64_t)n, i + (end - pos));
+        if (!first) __syncthreads();  // the previous tile's last dQ product has read sm.kt, sm.ds
+        first = false;
+        key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, i == 0 && i1 == n);
+        pos += i1 - i;
+        i = 0;
+        do {
+            if (++kt == nkt) kt = 0, ++bhk;
+        } while (pos < end && tile_steps(a.s, kt) == 0);
+    }
+}
+
+// The pre-kernel of the float32 backward: blocks below `rows_blocks` compute dsum and clear dQ
+// (bwd_pre_block); with a stream-K schedule each further block clears dK and dV of one key tile
+// that no single workgroup owns (split, or without steps: nobody writes it).
+__global__ __launch_bounds__(256) void bwd_pre_f32_kernel(BwdArgs a, StreamK sk, int rows_blocks) {
+    if ((int)blockIdx.x < rows_blocks) {
+        bwd_pre_block<float, true>(a, blockIdx.x);
+        return;
+    }
+    const AttnShape &s = a.s;
+    const int nkt = (s.S + kBN - 1) / kBN;
+    const int t = blockIdx.x - rows_blocks, bhk = t / nkt, kt = t % nkt;
+    int64_t ts = (int64_t)bhk * sk.per_kvh;
+    for (int k = 0; k < kt; ++k) ts += tile_steps(s, k);
+    const int n = tile_steps(s, kt);
+    if (n > 0 && chunk_of(sk, ts) == chunk_of(sk, ts + n - 1)) return;  // one owner stores it
+    const int n0 = kt * kBN, n1 = min(s.S, n0 + kBN);
+    const int64_t base = ((int64_t)bhk * s.S + n0) * s.E, count = (int64_t)(n1 - n0) * s.E;
+    float *dk = static_cast<float *>(a.dk) + base, *dv = static_cast<float *>(a.dv) + base;
+    for (int64_t j = threadIdx.x; j < count; j += 256) dk[j] = 0.f, dv[j] = 0.f;
+}
+
+// Workgroups of the backward that fit on the device at once (the occupancy the kernel's
+// waves_per_eu attribute sets: two per CU at D <= 64 without a mask, one otherwise); 0 if unknown.
+int resident_workgroups(int D, bool mask) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return cus * (D <= 64 && !mask ? 2 : 1);
+}
+
+// The stream-K schedule where whole tiles leave part of the device idle (measured on one MI355X,
+// dc_sdpa_bwd per call, whole tiles -> stream-K):
+//   * fewer key tiles than resident workgroups, or (causal, tiles of unequal work) as many:
+//     causal B1 H8 L2048 D64 405 -> 137 us, B1 H4 L8192 1592 -> 742 us, B8 H12 L512 149 -> 128
+//     us, B2 H16 L1024 D128 (256 tiles, 256 slots) 454 -> 315 us;
+//   * non-causal tiles (all of equal work) whose last wave is at most 3/4 full, up to 4 waves:
+//     B6 H16 L1024 D64 (1.5 waves) 652 -> 548 us.
+// With at least as many causal tiles as slots, whole tiles dealt longest first keep the device
+// busy (a CU left with one workgroup runs it nearly twice as fast), and the cut tiles' extra
+// prologues, atomics and clearing cost 2-6%: B8 H12 L1024 376 -> 391 us, B16 H16 L1024 828 ->
+// 879 us.  chunks == 0: whole tiles.
+StreamK plan_streamk(const AttnShape &s, int D) {
+    StreamK k{0, 0, 0};
+    const int nkt = (s.S + kBN - 1) / kBN;
+    for (int kt = 0; kt < nkt; ++kt) k.per_kvh += tile_steps(s, kt);
+    k.total = k.per_kvh * s.B * s.Hkv;
+    const int slots = resident_workgroups(D, s.mask != nullptr) & ~7;
+    if (slots < 8 || k.total == 0) return k;
+    const int64_t tiles = (int64_t)nkt * s.B * s.Hkv;
+    const int64_t last = tiles % slots;  // workgroups of the last, partial wave
+    const bool underfilled = s.causal ? tiles <= slots : tiles < slots;
+    const bool ragged = !s.causal && tiles < 4 * (int64_t)slots && last > 0 && 4 * last <= 3 * (int64_t)slots;
+    if (underfilled || ragged) k.chunks = slots;
+    return k;
+}
+
 template <int D, bool VEC>
-hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
+hipError_t launch_dv(const BwdArgs &a, const StreamK &sk, hipStream_t st) {
+    const bool mask = a.s.mask != nullptr;
+    if (sk.chunks > 0) {
+        const dim3 grid(sk.chunks), block(kThreads);
+        if (a.s.causal && mask) return launch(bwd_f32_streamk_kernel<D, true, true, VEC>, grid, block, st, a, sk);
+        if (a.s.causal) return launch(bwd_f32_streamk_kernel<D, true, false, VEC>, grid, block, st, a, sk);
+        if (mask) return launch(bwd_f32_streamk_kernel<D, false, true, VEC>, grid, block, st, a, sk);
+        return launch(bwd_f32_streamk_kernel<D, false, false, VEC>, grid, block, st, a, sk);
+    }
     const int nkt = (a.s.S + kBN - 1) / kBN;
     const dim3 grid(nkt * a.s.B * a.s.Hkv), block(kThreads);
-    const bool mask = a.s.mask != nullptr;
     if (a.s.causal && mask) return launch(bwd_f32_kernel<D, true, true, VEC>, grid, block, st, a);
     if (a.s.causal) return launch(bwd_f32_kernel<D, true, false, VEC>, grid, block, st, a);
     if (mask) return launch(bwd_f32_kernel<D, false, true, VEC>, grid, block, st, a);
@@ -361,17 +521,24 @@ template <int D>
 hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
     BwdArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked 16-byte alignment; E must fill D
-    return a.s.vec ? launch_dv<D, true>(a, st) : launch_dv<D, false>(a, st);
+    const StreamK sk = plan_streamk(a.s, D);
+    const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
+    const int rows_blocks = (int)((rows + 15) / 16);
+    const int64_t zero_blocks = sk.chunks > 0 ? (int64_t)a.s.B * a.s.Hkv * ((a.s.S + kBN - 1) / kBN) : 0;
+    if (rows_blocks + zero_blocks > 0)
+        return_if(launch(bwd_pre_f32_kernel, dim3((unsigned)(rows_blocks + zero_blocks)), dim3(256), st, a, sk,
+                         rows_blocks));
+    return a.s.vec ? launch_dv<D, true>(a, sk, st) : launch_dv<D, false>(a, sk, st);
 }
 
 }  // namespace
 
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st) {
-    const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
-    if (rows > 0) {
-        return_if(launch(bwd_pre_kernel<float, true>, dim3((rows + 15) / 16), dim3(256), st, a));
+    if (a.s.B * a.s.Hkv == 0 || a.s.S == 0) {
+        const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
+        if (rows > 0) return launch(bwd_pre_kernel<float, true>, dim3((rows + 15) / 16), dim3(256), st, a);
+        return hipSuccess;
     }
-    if (a.s.B * a.s.Hkv == 0 || a.s.S == 0) return hipSuccess;
     if (a.s.E <= 32) return launch_d<32>(a, st);
     if (a.s.E <= 64) return launch_d<64>(a, st);
     return launch_d<128>(a, st);

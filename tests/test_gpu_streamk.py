@@ -1,0 +1,79 @@
+"""GPU parity of the float32 backward under both of its schedules.
+
+The backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
+whole tiles would leave part of the device idle (fewer tiles than resident workgroups, or a
+ragged last wave of equal non-causal tiles), cuts the steps of all tiles into equal ranges, one
+per resident workgroup (stream-K).  A tile cut between ranges adds its dK / dV atomically into rows the pre-kernel
+cleared; tiles without steps (causal keys past the last query) are cleared there too.  These
+cases call the C ABI with dQ, dK and dV pre-filled with NaN, so a row neither schedule writes
+fails.  On MI355X (256 CUs) the shapes marked "whole" take the one-tile-per-workgroup grid, the
+others stream-K.  Tolerance, as for every float32 output: |gpu - ref| <= 2e-5 + 1e-5 |ref|.
+"""
+import numpy as np
+import pytest
+
+from tests._data import assert_f32
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _backward_nan_filled(g, q, k, v, out, lse, causal, mask=None):
+    from densecore_amd import _lib, _native
+    g, q, k, v, out, lse = (_t(x) for x in (g, q, k, v, out, lse))
+    dims = _native._attention_dims(q, k, v)
+    B, H, Hkv, L, S, E = dims
+    m, ms = _native._mask_arg(None if mask is None else _t(mask), dims, q.device)
+    dq = torch.full((B, H, L, E), float("nan"), device=DEV)
+    dk = torch.full((B, Hkv, S, E), float("nan"), device=DEV)
+    dv = torch.full((B, Hkv, S, E), float("nan"), device=DEV)
+    d = _native._desc(dims, causal, None, torch.float32, ms)
+    L_ = _lib.lib()
+    ws = _native._workspace(L_.dc_sdpa_bwd_workspace_size(d), q.device)
+    _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(g), _native._ptr(q), _native._ptr(k), _native._ptr(v),
+                              _native._ptr(out), _native._ptr(lse), _native._ptr(m), _native._ptr(dq),
+                              _native._ptr(dk), _native._ptr(dv), _native._ptr(ws), ws.numel(),
+                              _native._stream(q.device)))
+    torch.cuda.synchronize()
+    return [x.cpu().numpy() for x in (dq, dk, dv)]
+
+
+CASES = [  # tag, B, H, Hkv, L, S, E, causal, mask
+    ("c2_like", 2, 6, 6, 1024, 1024, 64, True, None),
+    ("causal_s_gt_l", 1, 4, 4, 300, 700, 64, True, None),     # tiles 3..5 have no steps
+    ("causal_l_gt_s", 2, 2, 2, 900, 260, 32, True, None),
+    ("noncausal_e128", 1, 3, 3, 500, 640, 128, False, None),
+    ("grouped", 2, 8, 2, 640, 640, 64, True, None),
+    ("masked_causal", 1, 2, 2, 384, 384, 64, True, "float"),
+    ("unaligned_e40", 1, 3, 3, 333, 333, 40, True, None),
+    ("ragged_noncausal", 6, 16, 16, 1024, 1024, 32, False, None),  # 1.5 waves of tiles
+    ("whole_causal", 16, 16, 16, 1024, 1024, 32, True, None),
+    ("whole_noncausal", 16, 16, 16, 512, 512, 32, False, None),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal,mask", CASES, ids=[c[0] for c in CASES])
+def test_backward_schedules(oracle_lib, tag, B, H, Hkv, L, S, E, causal, mask):
+    rng = np.random.default_rng(sum(map(ord, tag)))
+    q = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    g = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    m = None
+    if mask == "float":
+        m = rng.standard_normal((B, H, L, S), dtype=np.float32)
+        m[rng.random((B, H, L, S)) < 0.2] = -np.inf
+    print(f"[case] backward schedule {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}",
+          flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, None, m)
+    rq, rk, rv = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal, None, m)
+    dq, dk, dv = _backward_nan_filled(g, q, k, v, ref_o, ref_l, causal, m)
+    assert_f32(dq, rq, f"{tag} dq")
+    assert_f32(dk, rk, f"{tag} dk")
+    assert_f32(dv, rv, f"{tag} dv")
