@@ -98,6 +98,7 @@ size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv 
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
     size_t n = fwd_order_ws(s);
     if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s);
+    else n += round_up(dc::fwd_f32_split_bytes(s));
     return n;
 }
 
@@ -228,12 +229,17 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
-    // A workspace too small (or none) only gives up the longest-first order of key-padding masks
-    // and, for bf16, the fp16 P V product (the bf16 hi + lo pair is used instead).
+    // A workspace too small (or none) only gives up the longest-first order of key-padding masks,
+    // for float32 the split key ranges of small grids, and for bf16 the fp16 P V product (the
+    // bf16 hi + lo pair is used instead).
     char *ws = static_cast<char *>(workspace);
     if (mask && ws && workspace_bytes >= fwd_order_ws(s)) {
         a.tiles = reinterpret_cast<int *>(ws);
         a.order = a.tiles + (size_t)s.B * s.H;
+    }
+    if (d->dtype == DC_F32 && !mask && ws && workspace_bytes > fwd_order_ws(s)) {
+        a.split_o = reinterpret_cast<float *>(ws + fwd_order_ws(s));
+        a.split_bytes = workspace_bytes - fwd_order_ws(s);
     }
     if (d->dtype == DC_BF16 && !mask && ws && workspace_bytes >= fwd_ws(s, true)) {
         char *p = ws + fwd_order_ws(s);

@@ -116,7 +116,19 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
     }
 }
 
-template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC, bool ROWMASK = false>
+// Key tiles (of BN keys) query tile qt (of kBM queries) reads, and the pieces of `chunk` tiles it
+// runs as when key ranges are split (1 without a split).
+__host__ __device__ inline int fwd_tiles(const AttnShape &s, int kBM, int BN, int qt) {
+    const int kv_end = s.causal ? min((qt + 1) * kBM, s.S) : s.S;
+    return (kv_end + BN - 1) / BN;
+}
+__host__ __device__ inline int fwd_pieces(const AttnShape &s, int kBM, int BN, int qt, int chunk) {
+    if (chunk <= 0) return 1;
+    const int n = (fwd_tiles(s, kBM, BN, qt) + chunk - 1) / chunk;
+    return n > 1 ? n : 1;
+}
+
+template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC, bool ROWMASK = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     [[maybe_unused]] constexpr int kThreads = 64 * W;
     constexpr int kBM = 32 * W;
@@ -135,6 +147,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     const int bid = blockIdx.x;
     int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;  // longest causal tiles first
     int bh = bid % BH;
+    // Split key ranges: blocks run over (query tile, longest first; head; piece).
+    int piece = 0, npieces = 1;
+    if constexpr (SPLIT) {
+        int r = bid;
+        for (qt = nqt - 1; qt >= 0; --qt) {
+            const int np = fwd_pieces(s, kBM, BN, qt, a.split_chunk);
+            if (r < BH * np) {
+                bh = r / np, piece = r % np, npieces = np;
+                break;
+            }
+            r -= BH * np;
+        }
+        if (qt < 0) return;  // not reached: the grid holds exactly the pieces
+    }
     if (ROWMASK && a.order) {
         // Heads in descending order of live key tiles, dealt to the 8 XCDs round-robin (blocks
         // go to XCD bid % 8), the query tiles of one head on one XCD: its K/V stays in one L2.
@@ -194,14 +220,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
 
     const int kv_end = CAUSAL ? min(q0 + kBM, s.S) : s.S;
     const int ntiles = (kv_end + BN - 1) / BN;
+    // This block's key tiles [t_begin, t_end): all of them, or its piece's (the query tile's
+    // tiles cut into npieces near-equal ranges).
+    const int t_begin = SPLIT ? piece * ntiles / npieces : 0;
+    const int t_end = SPLIT ? (piece + 1) * ntiles / npieces : ntiles;
 
     KVStage<D, BN, W> stage;
     if constexpr (ASYNC) {
-        if (ntiles > 0) issue_tile<D, BN, W>(sm, kb, vb, 0, s.S, wave, lane);
-    } else if (s.vec && ntiles > 0) {
-        stage.load(kb, vb, 0, s.S, tid);
+        if (t_begin < t_end) issue_tile<D, BN, W>(sm, kb, vb, t_begin * BN, s.S, wave, lane);
+    } else if (s.vec && t_begin < t_end) {
+        stage.load(kb, vb, t_begin * BN, s.S, tid);
     }
-    if constexpr (ROWMASK) mask_next = row_mask(0);
+    if constexpr (ROWMASK) mask_next = row_mask(t_begin);
 
     // One tile per call; the asynchronous path alternates two distinct LDS objects so that
     // the compiler can see the in-flight loads never alias the tile being read.
@@ -220,7 +250,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
                 load_kv_generic<D, BN, W>(cur, kb, vb, n0, s.S, s.E, tid);
             }
             __syncthreads();
-            if (s.vec && t + 1 < ntiles) stage.load(kb, vb, n0 + BN, s.S, tid);
+            if (s.vec && t + 1 < t_end) stage.load(kb, vb, n0 + BN, s.S, tid);
         }
         // K row kr, dims d..d+3 (d a multiple of 4), and V row vr, dim d, of the current tile.
         auto kread = [&](int kr, int d) -> f32x4 {
@@ -370,18 +400,23 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
         }
     };
     if constexpr (ASYNC) {
-        for (int t = 0; t < ntiles; t += 2) {
-            tile(t, sm, sm2, t + 1 < ntiles ? t + 1 : -1);
-            if (t + 1 < ntiles) tile(t + 1, sm2, sm, t + 2 < ntiles ? t + 2 : -1);
+        for (int t = t_begin; t < t_end; t += 2) {
+            tile(t, sm, sm2, t + 1 < t_end ? t + 1 : -1);
+            if (t + 1 < t_end) tile(t + 1, sm2, sm, t + 2 < t_end ? t + 2 : -1);
         }
     } else {
-        for (int t = 0; t < ntiles; ++t) tile(t, sm, sm, -1);
+        for (int t = t_begin; t < t_end; ++t) tile(t, sm, sm, -1);
     }
 
     if (qi < s.L) {
         const bool empty = l_run == 0.f;
         const float inv = empty ? 0.f : 1.f / l_run;
-        float *orow = static_cast<float *>(a.out) + ((int64_t)bh * s.L + qi) * s.E;
+        const int64_t row = (int64_t)bh * s.L + qi;
+        // A piece of a split range writes its normalized partial and lse (-inf: no visible key)
+        // to the row's slot `piece`; fwd_split_merge_kernel combines them.
+        const bool partial = SPLIT && npieces > 1;
+        float *orow = partial ? a.split_o + (row * a.split_max + piece) * s.E
+                              : static_cast<float *>(a.out) + row * s.E;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -397,9 +432,63 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
                         if (d + u < s.E) orow[d + u] = oacc[dt][r + u] * inv;
                 }
             }
-        if (g == 0)
-            a.lse[(int64_t)bh * s.L + qi] = empty ? 0.f : (m_run + log2_fast(l_run)) * kLn2;
+        if (g == 0) {
+            if (partial)
+                a.split_lse[row * a.split_max + piece] = empty ? -INFINITY : (m_run + log2_fast(l_run)) * kLn2;
+            else
+                a.lse[row] = empty ? 0.f : (m_run + log2_fast(l_run)) * kLn2;
+        }
     }
+}
+
+// Combines the pieces of split query tiles, 16 lanes per query row: with the pieces' lse values
+// l_p and normalized outputs o_p, lse = log sum exp(l_p) and out = sum exp(l_p - lse) o_p.  A row
+// no piece sees any key of keeps the reference's out = 0, lse = 0.  Rows of query tiles that ran
+// whole were written by the forward and are skipped.  Each lane carries 4 consecutive dims of
+// each 64 (16-byte loads when rows are aligned), so a wave merges 4 rows with independent loads.
+__global__ __launch_bounds__(256) void fwd_split_merge_kernel(FwdArgs a, int kBM, int BN) {
+    const AttnShape &s = a.s;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    if (row >= (int64_t)s.B * s.H * s.L) return;
+    const int np = fwd_pieces(s, kBM, BN, (int)(row % s.L) / kBM, a.split_chunk);
+    if (np <= 1) return;
+    const float *pl = a.split_lse + row * a.split_max;
+    const float *po = a.split_o + row * a.split_max * s.E;
+    float *orow = static_cast<float *>(a.out) + row * s.E;
+    float mx = -INFINITY;
+    for (int p = 0; p < np; ++p) mx = fmaxf(mx, pl[p]);
+    if (mx == -INFINITY) {
+        for (int d = sub; d < s.E; d += 16) orow[d] = 0.f;
+        if (sub == 0) a.lse[row] = 0.f;
+        return;
+    }
+    float wsum = 0.f;
+    if (s.vec) {  // E is 32, 64 or 128 and rows are 16-byte aligned
+        const int d0 = 4 * sub;
+        const bool two = s.E > 64;
+        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int p = 0; p < np; ++p) {
+            const float w = expf(pl[p] - mx);
+            wsum += w;
+            const float *src = po + (int64_t)p * s.E;
+            if (d0 < s.E) acc0 += w * *reinterpret_cast<const f32x4 *>(src + d0);
+            if (two) acc1 += w * *reinterpret_cast<const f32x4 *>(src + 64 + d0);
+        }
+        const float inv = 1.f / wsum;
+        if (d0 < s.E) *reinterpret_cast<f32x4 *>(orow + d0) = acc0 * inv;
+        if (two) *reinterpret_cast<f32x4 *>(orow + 64 + d0) = acc1 * inv;
+    } else {
+        for (int p = 0; p < np; ++p) wsum += expf(pl[p] - mx);
+        const float inv = 1.f / wsum;
+        for (int d = sub; d < s.E; d += 16) {
+            float acc = 0.f;
+            for (int p = 0; p < np; ++p) acc = fmaf(expf(pl[p] - mx), po[(int64_t)p * s.E + d], acc);
+            orow[d] = acc * inv;
+        }
+    }
+    if (sub == 0) a.lse[row] = mx + logf(wsum);
 }
 
 // One wave per (b, h) of a query-independent mask: the number of BN-key tiles that hold any key
@@ -441,6 +530,61 @@ __global__ __launch_bounds__(1024) void rowmask_order_kernel(FwdArgs a, int ntil
     for (int i = tid; i < BH; i += 1024) a.order[atomicAdd(&start[a.tiles[i]], 1)] = i;
 }
 
+// Split key ranges where the whole-tile grid fills at most half of the workgroups that fit at
+// once (few heads, long rows): the key tiles of all query tiles are cut into pieces of `chunk`
+// tiles so that the pieces about fill the device.  chunk 0: no split.
+struct FwdSplitPlan {
+    int chunk = 0, max_pieces = 1;
+    int64_t blocks = 0;
+    size_t bytes = 0;
+};
+
+template <int D, int BN, int W>
+FwdSplitPlan plan_split(const AttnShape &s) {
+    FwdSplitPlan p;
+    if (s.mask != nullptr || s.L == 0 || s.S == 0) return p;
+    constexpr int kBM = 32 * W;
+    const int nqt = (s.L + kBM - 1) / kBM;
+    const int64_t BH = (int64_t)s.B * s.H;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return p;
+    if (2 * nqt * BH > 8 * (int64_t)cus) return p;  // no CU holds more than 8 such workgroups
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(&fwd_f32_kernel<D, BN, W, true, false, true, false, true>),
+            64 * W, 0) != hipSuccess)
+        return p;
+    const int64_t slots = (int64_t)cus * per_cu;
+    if (slots <= 0 || 2 * nqt * BH > slots) return p;
+    int64_t tiles = 0;
+    int most = 0;
+    for (int qt = 0; qt < nqt; ++qt) {
+        const int n = fwd_tiles(s, kBM, BN, qt);
+        tiles += n;
+        most = n > most ? n : most;
+    }
+    tiles *= BH;
+    // At least 4 key tiles per piece (a piece's fixed costs, its queries, the first tile's
+    // latency, the partial row and its merge, are then spread over 128+ keys), and no more
+    // pieces than slots: a second, partial wave of pieces would double the time.
+    int64_t chunk = (tiles + slots - 1) / slots;
+    for (chunk = chunk < 4 ? 4 : chunk; chunk < most; ++chunk) {
+        p.blocks = 0;
+        for (int qt = 0; qt < nqt; ++qt) p.blocks += BH * fwd_pieces(s, kBM, BN, qt, (int)chunk);
+        if (p.blocks <= slots) break;
+    }
+    if (chunk >= most) return FwdSplitPlan{};
+    p.chunk = (int)chunk;
+    for (int qt = 0; qt < nqt; ++qt) {
+        const int np = fwd_pieces(s, kBM, BN, qt, p.chunk);
+        p.max_pieces = np > p.max_pieces ? np : p.max_pieces;
+    }
+    const size_t rows = (size_t)BH * s.L * p.max_pieces;
+    p.bytes = rows * s.E * sizeof(float) + rows * sizeof(float);
+    return p;
+}
+
 template <int D, int BN, int W>
 hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     FwdArgs a = args;
@@ -448,6 +592,26 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     const int nqt = (a.s.L + 32 * W - 1) / (32 * W);
     const dim3 grid(nqt * a.s.B * a.s.H), block(64 * W);
     const bool mask = a.s.mask != nullptr;
+    if (a.split_o) {
+        const FwdSplitPlan p = plan_split<D, BN, W>(a.s);
+        if (p.chunk > 0 && p.bytes <= a.split_bytes) {
+            a.split_chunk = p.chunk, a.split_max = p.max_pieces;
+            a.split_lse = a.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
+            const dim3 sgrid((unsigned)p.blocks);
+            if (a.s.vec) {
+                if (a.s.causal)
+                    return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true, false, true>, sgrid, block, st, a));
+                else
+                    return_if(launch(fwd_f32_kernel<D, BN, W, false, false, true, false, true>, sgrid, block, st, a));
+            } else if (a.s.causal) {
+                return_if(launch(fwd_f32_kernel<D, BN, W, true, false, false, false, true>, sgrid, block, st, a));
+            } else {
+                return_if(launch(fwd_f32_kernel<D, BN, W, false, false, false, false, true>, sgrid, block, st, a));
+            }
+            const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
+            return launch(fwd_split_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, a, 32 * W, BN);
+        }
+    }
     if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
             return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a));
@@ -479,18 +643,43 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     return hipSuccess;
 }
 
+// The instantiation the forward runs for a shape: head dim D, key tile BN, waves W.  Short causal
+// problems take 2-wave workgroups over 32-key tiles: their causal work units are finer, which
+// balances the CUs better (measured on one MI355X: B64 H6 L256 D64 causal 54.0 -> 49.5 us; B8
+// H12 L1024 unchanged; non-causal B16 H16 L512 slower, 161 -> 171 us).  At D = 64 the 4-wave
+// workgroups take 32-key tiles: half the LDS of 64-key tiles (32 KB), so four workgroups fit a
+// CU instead of two (B8 H12 L1024 causal 148.7 -> 145.7 us, B2 H12 L4096 causal 480 -> 457 us).
+template <typename F>
+auto with_config(const AttnShape &s, F f) {
+    const bool small = s.causal && s.L <= 256;
+    if (s.E <= 32) return small ? f.template operator()<32, 32, 2>() : f.template operator()<32, 64, 4>();
+    if (s.E <= 64) return small ? f.template operator()<64, 32, 2>() : f.template operator()<64, 32, 4>();
+    return f.template operator()<128, 32, 4>();
+}
+
+struct SplitBytes {
+    const AttnShape &s;
+    template <int D, int BN, int W>
+    size_t operator()() const { return plan_split<D, BN, W>(s).bytes; }
+};
+
+struct Launch {
+    const FwdArgs &a;
+    hipStream_t st;
+    template <int D, int BN, int W>
+    hipError_t operator()() const { return launch_d<D, BN, W>(a, st); }
+};
+
 }  // namespace
+
+size_t fwd_f32_split_bytes(const AttnShape &s) {
+    if (s.B == 0 || s.H == 0 || s.L == 0) return 0;
+    return with_config(s, SplitBytes{s});
+}
 
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st) {
     if (a.s.B == 0 || a.s.H == 0 || a.s.L == 0) return hipSuccess;
-    // Short causal problems: 2-wave workgroups over 32-key tiles (four workgroups per CU).
-    // Their causal work units are finer, which balances the CUs better (measured on one MI355X:
-    // B64 H6 L256 D64 causal 54.0 -> 49.5 us; B8 H12 L1024 unchanged; non-causal B16 H16 L512
-    // slower, 161 -> 171 us).
-    const bool small = a.s.causal && a.s.L <= 256;
-    if (a.s.E <= 32) return small ? launch_d<32, 32, 2>(a, st) : launch_d<32, 64, 4>(a, st);
-    if (a.s.E <= 64) return small ? launch_d<64, 32, 2>(a, st) : launch_d<64, 64, 4>(a, st);
-    return launch_d<128, 32, 4>(a, st);
+    return with_config(a.s, Launch{a, st});
 }
 
 }  // namespace dc

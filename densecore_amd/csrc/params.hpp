@@ -32,6 +32,13 @@ struct FwdArgs {
     void *v16;
     float *f16_partial;
     int *vexp;
+    // Split key ranges (float32, no mask, grids that fill under half the device): query tiles
+    // of more than split_chunk key tiles run as pieces of split_chunk tiles, each writing its
+    // normalized partial output and lse, split_max slots per query row, merged afterwards.
+    // nullptr: no split.
+    float *split_o, *split_lse;
+    size_t split_bytes;  // bytes at split_o (split_lse included)
+    int split_chunk, split_max;
 };
 
 // Longest-first ordering of a key-padding mask's heads: used when the workspace holds it and
@@ -82,6 +89,9 @@ hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t sla
 
 // Each launcher returns hipSuccess or the launch error; it never synchronizes.
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st);
+// Workspace bytes the float32 forward uses to split key ranges on the current device (0: it
+// does not split this shape).
+size_t fwd_f32_split_bytes(const AttnShape &s);
 hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);

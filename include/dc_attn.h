@@ -67,9 +67,11 @@ int dc_abi_version(void);
 
 /* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  The workspace is
  * optional: it holds the longest-first workgroup order of a query-independent mask
- * (mask_stride_l == 0, e.g. key padding) and, for bf16 without a mask, the power-of-two-scaled
+ * (mask_stride_l == 0, e.g. key padding); for float32 without a mask, when the query tiles fill
+ * at most half of the current device, the partial outputs of split key ranges (so the size
+ * depends on the device current at the call); for bf16 without a mask, the power-of-two-scaled
  * fp16 copy of v that the P V product uses.  With less (or none) the forward runs in the natural
- * order and, for bf16, takes P as a bf16 hi + lo pair. */
+ * order, whole key ranges per query tile, and for bf16 takes P as a bf16 hi + lo pair. */
 size_t dc_sdpa_fwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const void *v,
                       const float *mask, void *out, float *lse, void *workspace,

@@ -1,6 +1,12 @@
-"""GPU parity of the float32 backward under both of its schedules.
+"""GPU parity of the float32 kernels under their alternative schedules.
 
-The backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
+Forward: when the grid of query tiles fills at most half of the workgroups that fit at once (few
+heads, long rows; no mask), the key tiles of each query tile run as pieces of at least 4 tiles,
+each writing a normalized partial output and lse, merged by a second kernel (rows of query tiles
+that ran whole are written directly).  The cases below take that path on MI355X; out and lse
+start as NaN, so a row neither path writes fails.
+
+Backward: the backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
 whole tiles would leave part of the device idle (fewer tiles than resident workgroups, or a
 ragged last wave of equal non-causal tiles), cuts the steps of all tiles into equal ranges, one
 per resident workgroup (stream-K).  A tile cut between ranges adds its dK / dV atomically into rows the pre-kernel
@@ -22,6 +28,48 @@ DEV = "cuda:0"
 
 def _t(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _forward_nan_filled(q, k, v, causal):
+    from densecore_amd import _lib, _native
+    q, k, v = (_t(x) for x in (q, k, v))
+    dims = _native._attention_dims(q, k, v)
+    B, H, Hkv, L, S, E = dims
+    out = torch.full((B, H, L, E), float("nan"), device=DEV)
+    lse = torch.full((B, H, L), float("nan"), device=DEV)
+    d = _native._desc(dims, causal, None, torch.float32, (0, 0, 0))
+    L_ = _lib.lib()
+    ws = _native._workspace(L_.dc_sdpa_fwd_workspace_size(d), q.device)
+    _lib.check(L_.dc_sdpa_fwd(d, _native._ptr(q), _native._ptr(k), _native._ptr(v), None,
+                              _native._ptr(out), _native._ptr(lse), _native._ptr(ws), ws.numel(),
+                              _native._stream(q.device)))
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), lse.cpu().numpy()
+
+
+FWD_CASES = [  # tag, B, H, Hkv, L, S, E, causal
+    ("causal_long", 1, 2, 2, 2048, 2048, 64, True),
+    ("full_l_ne_s", 1, 3, 3, 1500, 1700, 64, False),
+    ("causal_e128", 1, 2, 2, 700, 700, 128, True),
+    ("causal_e32", 1, 2, 2, 2048, 2048, 32, True),
+    ("grouped", 2, 4, 2, 1024, 1024, 64, True),
+    ("unaligned_e40", 1, 1, 1, 333, 2000, 40, False),
+    ("single_query", 1, 2, 2, 1, 5000, 64, False),
+    ("causal_l_gt_s", 1, 2, 2, 1200, 600, 64, True),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal", FWD_CASES, ids=[c[0] for c in FWD_CASES])
+def test_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
+    rng = np.random.default_rng(sum(map(ord, tag)) + 1)
+    q = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    print(f"[case] forward split {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    out, lse = _forward_nan_filled(q, k, v, causal)
+    assert_f32(out, ref_o, f"{tag} out")
+    assert_f32(lse, ref_l, f"{tag} lse")
 
 
 def _backward_nan_filled(g, q, k, v, out, lse, causal, mask=None):
