@@ -97,7 +97,7 @@ size_t fwd_partial_ws(const dc::AttnShape &s) {
 size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
     size_t n = fwd_order_ws(s);
-    if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s);
+    if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s) + round_up(dc::fwd_bf16_split_bytes(s));
     else n += round_up(dc::fwd_f32_split_bytes(s));
     return n;
 }
@@ -230,8 +230,8 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
     // A workspace too small (or none) only gives up the longest-first order of key-padding masks,
-    // for float32 the split key ranges of small grids, and for bf16 the fp16 P V product (the
-    // bf16 hi + lo pair is used instead).
+    // the split key ranges of small grids, and for bf16 the fp16 P V product (the bf16 hi + lo
+    // pair is used instead).
     char *ws = static_cast<char *>(workspace);
     if (mask && ws && workspace_bytes >= fwd_order_ws(s)) {
         a.tiles = reinterpret_cast<int *>(ws);
@@ -241,11 +241,16 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         a.split_o = reinterpret_cast<float *>(ws + fwd_order_ws(s));
         a.split_bytes = workspace_bytes - fwd_order_ws(s);
     }
-    if (d->dtype == DC_BF16 && !mask && ws && workspace_bytes >= fwd_ws(s, true)) {
+    const size_t bf16_copy = fwd_order_ws(s) + fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s);
+    if (d->dtype == DC_BF16 && !mask && ws && workspace_bytes >= bf16_copy) {
         char *p = ws + fwd_order_ws(s);
         a.v16 = p;
         a.f16_partial = reinterpret_cast<float *>(p + fwd_v16_ws(s));
         a.vexp = reinterpret_cast<int *>(p + fwd_v16_ws(s) + fwd_partial_ws(s));
+        if (workspace_bytes > bf16_copy) {
+            a.split_o = reinterpret_cast<float *>(ws + bf16_copy);
+            a.split_bytes = workspace_bytes - bf16_copy;
+        }
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (d->dtype == DC_F32) return launched(dc::launch_fwd_f32(a, strm));

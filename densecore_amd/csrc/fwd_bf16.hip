@@ -24,6 +24,7 @@
 //     the blocks of one (batch, head) run on the same XCD (blocks are dealt to the 8 XCDs
 //     round-robin), which keeps its K/V in that XCD's L2.
 #include "common.hpp"
+#include "fwd_split.hpp"
 #include "params.hpp"
 #include "tile_bf16.hpp"
 
@@ -288,7 +289,7 @@ constexpr int kPPM = 32 * kPPWaves;  // queries per workgroup
 
 // F16V: V is the fp16 copy (scaled by 2^vexp[b, kv head]) and P is rounded once to fp16, so the
 // P V product is one fp16 MFMA per fragment instead of the bf16 hi + lo pair.
-template <int D, bool CAUSAL, bool VEC, bool F16V>
+template <int D, bool CAUSAL, bool VEC, bool F16V, bool SPLIT = false>
 __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_pp_kernel(FwdArgs a) {
     constexpr int NT = kBN / 32, KSTEP = D / 16, NDT = D / 32;
     __shared__ KVTileBf16<D> sm[2];
@@ -299,7 +300,12 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     const int grp = wave >> 2;
     const int nqt = (s.L + kPPM - 1) / kPPM;
     const int w = logical_block();
-    const int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    // Split key ranges: blocks run over (head, query tile longest first, piece) (fwd_split.hpp).
+    int piece = 0, npieces = 1;
+    if constexpr (SPLIT) {
+        if (!split_block(s, kPPM, kBN, a.split_chunk, w, &qt, &bh, &piece, &npieces)) return;
+    }
     const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
     const int q0 = qt * kPPM;
     const int wave_q0 = q0 + grp * 128 + (wave & 3) * 32, wave_last_q = wave_q0 + 31;
@@ -342,6 +348,9 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 
     const int kv_end = CAUSAL ? min(q0 + kPPM, s.S) : s.S;
     const int ntiles = (kv_end + kBN - 1) / kBN;
+    // This block's key tiles [t_begin, t_end): all of them, or its piece's.
+    const int t_begin = SPLIT ? piece * ntiles / npieces : 0;
+    const int t_end = SPLIT ? (piece + 1) * ntiles / npieces : ntiles;
     const uint32_t rowb = row_lanebase<kBN, D>(lane);
     const uint32_t trb = tr_lanebase<kBN, D>(lane);
 
@@ -360,7 +369,7 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     // PV(t-1) first, then S(t): P's registers are dead before S is written, so the two share
     // registers.
     auto gemm = [&](int t) {
-        if (t >= 1 && sub_live(t - 1, 0)) {
+        if (t > t_begin && sub_live(t - 1, 0)) {
             const u32x4 *vt_ = sm[(t - 1) & 1].v;
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) {
@@ -382,7 +391,7 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
             }
         }
-        if (t < ntiles && sub_live(t, 0)) {
+        if (t < t_end && sub_live(t, 0)) {
             const u32x4 *kt_ = sm[t & 1].k;
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt)
@@ -400,7 +409,7 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     // l are rescaled) only when some lane's tile max exceeds it by more than 8, so P <= 2^8;
     // out = O / l and lse = m_run + log2(l) are exact either way.
     auto softmax = [&](int t) {
-        if (t >= ntiles || !sub_live(t, 0)) return;
+        if (t >= t_end || !sub_live(t, 0)) return;
         const int n0 = t * kBN;
         if (n0 + kBN > s.S || (CAUSAL && n0 + kBN - 1 > wave_q0)) {
             // Register r of sub-tile kt holds key n0 + 32 kt + 4g + (8 (r/4) + r%4).
@@ -450,17 +459,17 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 
     // fill(t) at phase 2t: K(t + 1) into K(t - 1)'s buffer, V(t) into V(t - 2)'s buffer.
     auto fill = [&](int t) {
-        if (t + 1 < ntiles) fill_k(t + 1);
-        if (t < ntiles) fill_v(t);
+        if (t + 1 < t_end) fill_k(t + 1);
+        if (t < t_end) fill_v(t);
     };
-    if (ntiles > 0) fill_k(0);
+    if (t_begin < t_end) fill_k(t_begin);
     if (VEC) wait_vmem();
     __syncthreads();
     // Phases 0 .. 2 ntiles + 1, one barrier each; the transfers issued at an even phase are
     // waited for at the end of the next (odd) one.  Each group has its own loop, so that only
     // the registers of S (group 1) or of P (group 0) are carried from one iteration to the next.
     if (grp == 0) {
-        for (int t = 0; t <= ntiles; ++t) {
+        for (int t = t_begin; t <= t_end; ++t) {
             fill(t);
             gemm(t);
             __syncthreads();
@@ -469,9 +478,9 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             __syncthreads();
         }
     } else {
-        for (int t = 0; t <= ntiles; ++t) {
+        for (int t = t_begin; t <= t_end; ++t) {
             fill(t);
-            if (t >= 1) softmax(t - 1);
+            if (t > t_begin) softmax(t - 1);
             __syncthreads();
             gemm(t);
             if (VEC) wait_vmem();
@@ -480,6 +489,34 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 
     const float l_run = xor32_add(l_part);
+    if (SPLIT && npieces > 1) {
+        // A piece of a split range: its normalized partial (float32) and lse (-inf: no visible
+        // key) go to the row's slot `piece`; fwd_split_merge_kernel combines them.
+        if (qi < s.L) {
+            const bool empty = l_run == 0.f;
+            float inv = empty ? 0.f : 1.f / l_run;
+            if constexpr (F16V) inv = ldexpf(inv, -a.vexp[b * s.Hkv + hk]);
+            const int64_t row = (int64_t)bh * s.L + qi;
+            float *prow = a.split_o + (row * a.split_max + piece) * s.E;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; r += 4) {
+                    const int d = dt * 32 + acc_row(r, g);
+                    if (VEC) {
+                        *reinterpret_cast<f32x4 *>(prow + d) = f32x4{oacc[dt][r] * inv, oacc[dt][r + 1] * inv,
+                                                                     oacc[dt][r + 2] * inv, oacc[dt][r + 3] * inv};
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            if (d + u < s.E) prow[d + u] = oacc[dt][r + u] * inv;
+                    }
+                }
+            if (g == 0)
+                a.split_lse[row * a.split_max + piece] = empty ? -INFINITY : (m_run + log2_fast(l_run)) * kLn2;
+        }
+        return;
+    }
     if (qi < s.L) {
         const bool empty = l_run == 0.f;
         float inv = empty ? 0.f : 1.f / l_run;
@@ -507,6 +544,15 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 }
 
+// The split of the unmasked (ping-pong, fp16 P V) forward's grid on the current device.
+template <int D>
+FwdSplitPlan plan(const AttnShape &s) {
+    const int64_t blocks = (int64_t)(s.L + kPPM - 1) / kPPM * s.B * s.H;
+    const int64_t slots = split_slots(reinterpret_cast<const void *>(&fwd_bf16_pp_kernel<D, true, true, true, true>),
+                                      kPPThreads, blocks);
+    return plan_split(s, kPPM, kBN, slots);
+}
+
 template <int D, bool VEC>
 hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
     const bool mask = a.s.mask != nullptr;
@@ -518,6 +564,21 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
             return_if(launch_to_f16(a.v, a.v16, (int64_t)a.s.B * a.s.Hkv, (int64_t)a.s.S * a.s.E,
                                     a.f16_partial, a.vexp, st));
             f.v = a.v16;
+            if (a.split_o) {
+                const FwdSplitPlan p = plan<D>(a.s);
+                if (p.chunk > 0 && p.bytes <= a.split_bytes) {
+                    f.split_chunk = p.chunk, f.split_max = p.max_pieces;
+                    f.split_lse = f.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
+                    const dim3 sgrid((unsigned)p.blocks);
+                    if (a.s.causal)
+                        return_if(launch(fwd_bf16_pp_kernel<D, true, VEC, true, true>, sgrid, block, st, f));
+                    else
+                        return_if(launch(fwd_bf16_pp_kernel<D, false, VEC, true, true>, sgrid, block, st, f));
+                    const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
+                    return launch(fwd_split_merge_kernel<__bf16>, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, f,
+                                  kPPM, kBN);
+                }
+            }
             if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, true>, grid, block, st, f);
             return launch(fwd_bf16_pp_kernel<D, false, VEC, true>, grid, block, st, f);
         }
@@ -538,6 +599,13 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
 }
 
 }  // namespace
+
+size_t fwd_bf16_split_bytes(const AttnShape &s) {
+    if (s.B == 0 || s.H == 0 || s.L == 0) return 0;
+    if (s.E <= 32) return plan<32>(s).bytes;
+    if (s.E <= 64) return plan<64>(s).bytes;
+    return plan<128>(s).bytes;
+}
 
 hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st) {
     if (a.s.B == 0 || a.s.H == 0 || a.s.L == 0) return hipSuccess;

@@ -20,6 +20,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "fwd_split.hpp"
 #include "params.hpp"
 
 namespace dc {
@@ -116,18 +117,6 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
     }
 }
 
-// Key tiles (of BN keys) query tile qt (of kBM queries) reads, and the pieces of `chunk` tiles it
-// runs as when key ranges are split (1 without a split).
-__host__ __device__ inline int fwd_tiles(const AttnShape &s, int kBM, int BN, int qt) {
-    const int kv_end = s.causal ? min((qt + 1) * kBM, s.S) : s.S;
-    return (kv_end + BN - 1) / BN;
-}
-__host__ __device__ inline int fwd_pieces(const AttnShape &s, int kBM, int BN, int qt, int chunk) {
-    if (chunk <= 0) return 1;
-    const int n = (fwd_tiles(s, kBM, BN, qt) + chunk - 1) / chunk;
-    return n > 1 ? n : 1;
-}
-
 template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC, bool ROWMASK = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     [[maybe_unused]] constexpr int kThreads = 64 * W;
@@ -147,19 +136,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     const int bid = blockIdx.x;
     int qt = CAUSAL ? nqt - 1 - bid / BH : bid / BH;  // longest causal tiles first
     int bh = bid % BH;
-    // Split key ranges: blocks run over (query tile, longest first; head; piece).
+    // Split key ranges: blocks run over (head, query tile longest first, piece), the pieces of a
+    // head dealt to one XCD (blocks go to XCD bid % 8) so that its K/V stays in one L2.
     int piece = 0, npieces = 1;
     if constexpr (SPLIT) {
-        int r = bid;
-        for (qt = nqt - 1; qt >= 0; --qt) {
-            const int np = fwd_pieces(s, kBM, BN, qt, a.split_chunk);
-            if (r < BH * np) {
-                bh = r / np, piece = r % np, npieces = np;
-                break;
-            }
-            r -= BH * np;
-        }
-        if (qt < 0) return;  // not reached: the grid holds exactly the pieces
+        const int n = gridDim.x, w = (n & 7) == 0 ? (bid & 7) * (n >> 3) + (bid >> 3) : bid;
+        if (!split_block(s, kBM, BN, a.split_chunk, w, &qt, &bh, &piece, &npieces)) return;
     }
     if (ROWMASK && a.order) {
         // Heads in descending order of live key tiles, dealt to the 8 XCDs round-robin (blocks
@@ -441,56 +423,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     }
 }
 
-// Combines the pieces of split query tiles, 16 lanes per query row: with the pieces' lse values
-// l_p and normalized outputs o_p, lse = log sum exp(l_p) and out = sum exp(l_p - lse) o_p.  A row
-// no piece sees any key of keeps the reference's out = 0, lse = 0.  Rows of query tiles that ran
-// whole were written by the forward and are skipped.  Each lane carries 4 consecutive dims of
-// each 64 (16-byte loads when rows are aligned), so a wave merges 4 rows with independent loads.
-__global__ __launch_bounds__(256) void fwd_split_merge_kernel(FwdArgs a, int kBM, int BN) {
-    const AttnShape &s = a.s;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int sub = threadIdx.x & 15;
-    if (row >= (int64_t)s.B * s.H * s.L) return;
-    const int np = fwd_pieces(s, kBM, BN, (int)(row % s.L) / kBM, a.split_chunk);
-    if (np <= 1) return;
-    const float *pl = a.split_lse + row * a.split_max;
-    const float *po = a.split_o + row * a.split_max * s.E;
-    float *orow = static_cast<float *>(a.out) + row * s.E;
-    float mx = -INFINITY;
-    for (int p = 0; p < np; ++p) mx = fmaxf(mx, pl[p]);
-    if (mx == -INFINITY) {
-        for (int d = sub; d < s.E; d += 16) orow[d] = 0.f;
-        if (sub == 0) a.lse[row] = 0.f;
-        return;
-    }
-    float wsum = 0.f;
-    if (s.vec) {  // E is 32, 64 or 128 and rows are 16-byte aligned
-        const int d0 = 4 * sub;
-        const bool two = s.E > 64;
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int p = 0; p < np; ++p) {
-            const float w = expf(pl[p] - mx);
-            wsum += w;
-            const float *src = po + (int64_t)p * s.E;
-            if (d0 < s.E) acc0 += w * *reinterpret_cast<const f32x4 *>(src + d0);
-            if (two) acc1 += w * *reinterpret_cast<const f32x4 *>(src + 64 + d0);
-        }
-        const float inv = 1.f / wsum;
-        if (d0 < s.E) *reinterpret_cast<f32x4 *>(orow + d0) = acc0 * inv;
-        if (two) *reinterpret_cast<f32x4 *>(orow + 64 + d0) = acc1 * inv;
-    } else {
-        for (int p = 0; p < np; ++p) wsum += expf(pl[p] - mx);
-        const float inv = 1.f / wsum;
-        for (int d = sub; d < s.E; d += 16) {
-            float acc = 0.f;
-            for (int p = 0; p < np; ++p) acc = fmaf(expf(pl[p] - mx), po[(int64_t)p * s.E + d], acc);
-            orow[d] = acc * inv;
-        }
-    }
-    if (sub == 0) a.lse[row] = mx + logf(wsum);
-}
-
 // One wave per (b, h) of a query-independent mask: the number of BN-key tiles that hold any key
 // whose mask is not -inf (the tiles the forward computes; the others it skips).
 template <int BN>
@@ -530,59 +462,13 @@ __global__ __launch_bounds__(1024) void rowmask_order_kernel(FwdArgs a, int ntil
     for (int i = tid; i < BH; i += 1024) a.order[atomicAdd(&start[a.tiles[i]], 1)] = i;
 }
 
-// Split key ranges where the whole-tile grid fills at most half of the workgroups that fit at
-// once (few heads, long rows): the key tiles of all query tiles are cut into pieces of `chunk`
-// tiles so that the pieces about fill the device.  chunk 0: no split.
-struct FwdSplitPlan {
-    int chunk = 0, max_pieces = 1;
-    int64_t blocks = 0;
-    size_t bytes = 0;
-};
-
+// The split of this instantiation's grid on the current device (fwd_split.hpp).
 template <int D, int BN, int W>
-FwdSplitPlan plan_split(const AttnShape &s) {
-    FwdSplitPlan p;
-    if (s.mask != nullptr || s.L == 0 || s.S == 0) return p;
-    constexpr int kBM = 32 * W;
-    const int nqt = (s.L + kBM - 1) / kBM;
-    const int64_t BH = (int64_t)s.B * s.H;
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return p;
-    if (2 * nqt * BH > 8 * (int64_t)cus) return p;  // no CU holds more than 8 such workgroups
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(&fwd_f32_kernel<D, BN, W, true, false, true, false, true>),
-            64 * W, 0) != hipSuccess)
-        return p;
-    const int64_t slots = (int64_t)cus * per_cu;
-    if (slots <= 0 || 2 * nqt * BH > slots) return p;
-    int64_t tiles = 0;
-    int most = 0;
-    for (int qt = 0; qt < nqt; ++qt) {
-        const int n = fwd_tiles(s, kBM, BN, qt);
-        tiles += n;
-        most = n > most ? n : most;
-    }
-    tiles *= BH;
-    // At least 4 key tiles per piece (a piece's fixed costs, its queries, the first tile's
-    // latency, the partial row and its merge, are then spread over 128+ keys), and no more
-    // pieces than slots: a second, partial wave of pieces would double the time.
-    int64_t chunk = (tiles + slots - 1) / slots;
-    for (chunk = chunk < 4 ? 4 : chunk; chunk < most; ++chunk) {
-        p.blocks = 0;
-        for (int qt = 0; qt < nqt; ++qt) p.blocks += BH * fwd_pieces(s, kBM, BN, qt, (int)chunk);
-        if (p.blocks <= slots) break;
-    }
-    if (chunk >= most) return FwdSplitPlan{};
-    p.chunk = (int)chunk;
-    for (int qt = 0; qt < nqt; ++qt) {
-        const int np = fwd_pieces(s, kBM, BN, qt, p.chunk);
-        p.max_pieces = np > p.max_pieces ? np : p.max_pieces;
-    }
-    const size_t rows = (size_t)BH * s.L * p.max_pieces;
-    p.bytes = rows * s.E * sizeof(float) + rows * sizeof(float);
-    return p;
+FwdSplitPlan plan(const AttnShape &s) {
+    const int64_t blocks = (int64_t)(s.L + 32 * W - 1) / (32 * W) * s.B * s.H;
+    const int64_t slots = split_slots(
+        reinterpret_cast<const void *>(&fwd_f32_kernel<D, BN, W, true, false, true, false, true>), 64 * W, blocks);
+    return plan_split(s, 32 * W, BN, slots);
 }
 
 template <int D, int BN, int W>
@@ -593,7 +479,7 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     const dim3 grid(nqt * a.s.B * a.s.H), block(64 * W);
     const bool mask = a.s.mask != nullptr;
     if (a.split_o) {
-        const FwdSplitPlan p = plan_split<D, BN, W>(a.s);
+        const FwdSplitPlan p = plan<D, BN, W>(a.s);
         if (p.chunk > 0 && p.bytes <= a.split_bytes) {
             a.split_chunk = p.chunk, a.split_max = p.max_pieces;
             a.split_lse = a.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
@@ -609,7 +495,8 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
                 return_if(launch(fwd_f32_kernel<D, BN, W, false, false, false, false, true>, sgrid, block, st, a));
             }
             const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
-            return launch(fwd_split_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, a, 32 * W, BN);
+            return launch(fwd_split_merge_kernel<float>, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, a,
+                          32 * W, BN);
         }
     }
     if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
@@ -660,7 +547,7 @@ auto with_config(const AttnShape &s, F f) {
 struct SplitBytes {
     const AttnShape &s;
     template <int D, int BN, int W>
-    size_t operator()() const { return plan_split<D, BN, W>(s).bytes; }
+    size_t operator()() const { return plan<D, BN, W>(s).bytes; }
 };
 
 struct Launch {

@@ -32,7 +32,7 @@ struct FwdArgs {
     void *v16;
     float *f16_partial;
     int *vexp;
-    // Split key ranges (float32, no mask, grids that fill under half the device): query tiles
+    // Split key ranges (no mask, grids that fill under half the device): query tiles
     // of more than split_chunk key tiles run as pieces of split_chunk tiles, each writing its
     // normalized partial output and lse, split_max slots per query row, merged afterwards.
     // nullptr: no split.
@@ -93,6 +93,8 @@ hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st);
 // does not split this shape).
 size_t fwd_f32_split_bytes(const AttnShape &s);
 hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st);
+// The same for the bf16 forward (its unmasked path with the fp16 copy of V).
+size_t fwd_bf16_split_bytes(const AttnShape &s);
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);
 hipError_t launch_decode(const DecodeArgs &a, bool bf16, hipStream_t st);

@@ -1,7 +1,8 @@
-"""GPU parity of the float32 kernels under their alternative schedules.
+"""GPU parity of the kernels under their alternative schedules.
 
-Forward: when the grid of query tiles fills at most half of the workgroups that fit at once (few
-heads, long rows; no mask), the key tiles of each query tile run as pieces of at least 4 tiles,
+Forward (float32, and bf16 with its fp16 copy of V): when the grid of query tiles fills at most
+half of the workgroups that fit at once (few heads, long rows; no mask), the key tiles of each
+query tile run as pieces of at least 4 tiles,
 each writing a normalized partial output and lse, merged by a second kernel (rows of query tiles
 that ran whole are written directly).  The cases below take that path on MI355X; out and lse
 start as NaN, so a row neither path writes fails.
@@ -18,7 +19,7 @@ others stream-K.  Tolerance, as for every float32 output: |gpu - ref| <= 2e-5 + 
 import numpy as np
 import pytest
 
-from tests._data import assert_f32
+from tests._data import assert_bf16, assert_f32, bf16_round
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -30,21 +31,22 @@ def _t(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
 
 
-def _forward_nan_filled(q, k, v, causal):
+def _forward_nan_filled(q, k, v, causal, dtype=None):
     from densecore_amd import _lib, _native
-    q, k, v = (_t(x) for x in (q, k, v))
+    dtype = dtype or torch.float32
+    q, k, v = (_t(x).to(dtype) for x in (q, k, v))
     dims = _native._attention_dims(q, k, v)
     B, H, Hkv, L, S, E = dims
-    out = torch.full((B, H, L, E), float("nan"), device=DEV)
+    out = torch.full((B, H, L, E), float("nan"), device=DEV, dtype=dtype)
     lse = torch.full((B, H, L), float("nan"), device=DEV)
-    d = _native._desc(dims, causal, None, torch.float32, (0, 0, 0))
+    d = _native._desc(dims, causal, None, dtype, (0, 0, 0))
     L_ = _lib.lib()
     ws = _native._workspace(L_.dc_sdpa_fwd_workspace_size(d), q.device)
     _lib.check(L_.dc_sdpa_fwd(d, _native._ptr(q), _native._ptr(k), _native._ptr(v), None,
                               _native._ptr(out), _native._ptr(lse), _native._ptr(ws), ws.numel(),
                               _native._stream(q.device)))
     torch.cuda.synchronize()
-    return out.cpu().numpy(), lse.cpu().numpy()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
 
 
 FWD_CASES = [  # tag, B, H, Hkv, L, S, E, causal
@@ -70,6 +72,31 @@ def test_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
     out, lse = _forward_nan_filled(q, k, v, causal)
     assert_f32(out, ref_o, f"{tag} out")
     assert_f32(lse, ref_l, f"{tag} lse")
+
+
+BF16_FWD_CASES = [  # tag, B, H, Hkv, L, S, E, causal (256-query tiles, 64-key tiles)
+    ("causal_e128", 1, 2, 2, 2048, 2048, 128, True),
+    ("full_e64", 1, 1, 1, 1000, 4096, 64, False),
+    ("grouped_e128", 1, 4, 2, 1024, 1024, 128, True),
+    ("causal_e32", 2, 1, 1, 1536, 1536, 32, True),
+    ("unaligned_e40", 1, 1, 1, 700, 2500, 40, False),
+    ("single_query", 1, 3, 3, 1, 5000, 128, False),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal", BF16_FWD_CASES, ids=[c[0] for c in BF16_FWD_CASES])
+def test_bf16_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
+    """The bf16 forward's split path (fp16 P V product, pieces merged into bf16 out) against the
+    oracle on the bf16-rounded inputs, to the bf16 bar |gpu - ref| <= 1e-2 |ref| + 1e-2 rms."""
+    rng = np.random.default_rng(sum(map(ord, tag)) + 2)
+    q = bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32))
+    k = bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32))
+    v = bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32))
+    print(f"[case] bf16 forward split {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    out, lse = _forward_nan_filled(q, k, v, causal, torch.bfloat16)
+    assert_bf16(out, ref_o, f"{tag} out")
+    assert_bf16(lse, ref_l, f"{tag} lse")
 
 
 def _backward_nan_filled(g, q, k, v, out, lse, causal, mask=None):
