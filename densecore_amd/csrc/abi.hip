@@ -103,9 +103,10 @@ size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
 }
 
 // The backward's workspace: dsum (B*H*L floats; float32 accumulates dQ in its output), then for
-// bf16 the scaled fp16 copies of q, k, v, dout with their per-slab scratch.
+// bf16 the scaled fp16 copies of q, k, v, dout with their per-slab scratch, then the float32
+// partials of split grids (small grids on the current device; none otherwise).
 struct BwdLayout {
-    size_t dsum, q16, k16, v16, do16, partial, exps, total;
+    size_t dsum, q16, k16, v16, do16, partial, exps, copies_end, split, total;
 };
 BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     BwdLayout l{};
@@ -126,6 +127,8 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
         l.v16 = take(nk * 2);
         l.partial = take((size_t)s.B * s.Hkv * parts * sizeof(float));
         l.exps = take((size_t)4 * s.B * s.Hkv * sizeof(int));
+        l.copies_end = at;
+        l.split = take(dc::bwd_bf16_split_bytes(s));
     }
     l.total = at;
     return l;
@@ -291,11 +294,15 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     a.dsum = reinterpret_cast<float *>(ws);
     a.dq_acc = bf16 ? nullptr : static_cast<float *>(dq);
     // bf16: the fp16 products when the workspace holds the copies (else the bf16 hi + lo pairs).
-    if (bf16 && workspace_bytes >= bwd_ws(s, true)) {
-        const BwdLayout l = bwd_layout(s, true);
+    const BwdLayout l = bwd_layout(s, bf16);
+    if (bf16 && workspace_bytes >= l.copies_end) {
         a.q16 = ws + l.q16, a.k16 = ws + l.k16, a.v16 = ws + l.v16, a.do16 = ws + l.do16;
         a.f16_partial = reinterpret_cast<float *>(ws + l.partial);
         a.exps = reinterpret_cast<int *>(ws + l.exps);
+        if (l.total > l.split && workspace_bytes >= l.total) {
+            a.split = reinterpret_cast<float *>(ws + l.split);
+            a.split_bytes = l.total - l.split;
+        }
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (!bf16) return launched(dc::launch_bwd_f32(a, strm));

@@ -28,10 +28,12 @@
 // A row read (lanes = 32 consecutive rows, one chunk) is 512 contiguous bytes, and a
 // transposed read (8 rows x 4 chunks x 8 bytes) hits every bank exactly twice; all inner-loop
 // addresses are a per-lane base plus a constant.
+#include <algorithm>
 #include <type_traits>
 
 #include "bwd_common.hpp"
 #include "common.hpp"
+#include "fwd_split.hpp"
 #include "params.hpp"
 #include "tile_bf16.hpp"
 
@@ -98,7 +100,20 @@ DEVI f32x16 mfma16(bf16x8 x, bf16x8 y, f32x16 c) {
     else return mfma_bf16(x, y, c);
 }
 
-template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16>
+// Query steps (of kKM queries, over the query heads sharing the kv head) of key tile kt, and the
+// pieces of at most `chunk` steps it runs as when split (1 without a split).
+__host__ __device__ inline int dkdv_steps(const AttnShape &s, int kt) {
+    const int m_begin = s.causal ? kt * kKN : 0;  // a multiple of kKM
+    const int per_head = s.L > m_begin ? (s.L - m_begin + kKM - 1) / kKM : 0;
+    return per_head * s.repeat;
+}
+__host__ __device__ inline int dkdv_pieces(const AttnShape &s, int kt, int chunk) {
+    if (chunk <= 0) return 1;
+    const int n = (dkdv_steps(s, kt) + chunk - 1) / chunk;
+    return n > 1 ? n : 1;
+}
+
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16, bool SPLIT = false>
 __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32;
     __shared__ DkdvSmem<D> sm;
@@ -109,7 +124,23 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     const int kw = wave & 3, qh = wave >> 2;
     const int nkt = (s.S + kKN - 1) / kKN;
     const int w = logical_block();
-    const int bhk = w / nkt, n0 = (w % nkt) * kKN;  // causal: small n0 (most queries) first
+    int bhk = w / nkt, kt_ = w % nkt;  // causal: small n0 (most queries) first
+    // Split: blocks run over (kv head, key tile, piece), the pieces of a key tile adjacent.
+    int piece = 0, npieces = 1;
+    if constexpr (SPLIT) {
+        int per = 0;
+        for (int t = 0; t < nkt; ++t) per += dkdv_pieces(s, t, a.chunk_k);
+        bhk = w / per;
+        int r = w % per;
+        for (kt_ = 0; kt_ < nkt; ++kt_) {
+            const int np = dkdv_pieces(s, kt_, a.chunk_k);
+            if (r < np) break;
+            r -= np;
+        }
+        if (bhk >= s.B * s.Hkv || kt_ >= nkt) return;  // not reached: the grid holds the pieces
+        piece = r, npieces = dkdv_pieces(s, kt_, a.chunk_k);
+    }
+    const int n0 = kt_ * kKN;
     const int b = bhk / s.Hkv, hk = bhk % s.Hkv;
     const int kw0 = n0 + 32 * kw;
     const int key = kw0 + lr;  // this lane's key column
@@ -125,7 +156,10 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 
     const int m_begin = CAUSAL ? n0 : 0;  // n0 is a multiple of kKM
     const int per_head = s.L > m_begin ? (s.L - m_begin + kKM - 1) / kKM : 0;
-    const int nsteps = per_head * s.repeat;
+    const int all_steps = per_head * s.repeat;
+    // This block's steps [i_begin, nsteps): all of them, or its piece's.
+    const int i_begin = SPLIT ? piece * all_steps / npieces : 0;
+    const int nsteps = SPLIT ? (piece + 1) * all_steps / npieces : all_steps;
     auto step_bh = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
     auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kKM; };
     auto fill_step = [&](int i) {
@@ -148,9 +182,9 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         if (wave == 0) sm.m.lse[i & 1][lane] = x;
         else sm.m.dsum[i & 1][lane] = x;
     };
-    if (nsteps > 0) {
-        fill_step(0);
-        if (wave < 2) store_row_stat(0, load_row_stat(0));
+    if (i_begin < nsteps) {
+        fill_step(i_begin);
+        if (wave < 2) store_row_stat(i_begin, load_row_stat(i_begin));
     }
 
     const uint32_t rowb = row_lanebase<kKM, D>(lane);
@@ -163,7 +197,7 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[dt][r] = 0.f, dv[dt][r] = 0.f;
 
-    for (int i = 0; i < nsteps; ++i) {
+    for (int i = i_begin; i < nsteps; ++i) {
         const int bh = step_bh(i), h = bh - b * s.H, m0 = step_m0(i), buf = i & 1;
         if (VEC) wait_vmem();
         __syncthreads();  // step i's tiles landed (and K/V at i = 0); step i - 1 is done
@@ -278,6 +312,27 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                 dv[dt][r] = ldexpf(dv[dt][r], -fs.e_do);
             }
         }
+    if (SPLIT && npieces > 1) {
+        // A piece: its float32 partials go to slot `piece` of the key's rows
+        // (bwd_split_reduce_kernel sums them).
+        const size_t nrows = (size_t)s.B * s.Hkv * s.S;
+        const int64_t row = (int64_t)bhk * s.S + key;
+        float *pk = a.split + ((size_t)piece * nrows + row) * s.E;
+        float *pv = a.split + ((size_t)(a.max_k + piece) * nrows + row) * s.E;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+                const int d = dt * 32 + acc_row(r, g);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (d + u < s.E) {
+                        pk[d + u] = dk[dt][r + u] * s.scale;
+                        pv[d + u] = dv[dt][r + u];
+                    }
+            }
+        return;
+    }
     __bf16 *dkr = static_cast<__bf16 *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
     __bf16 *dvr = static_cast<__bf16 *>(a.dv) + ((int64_t)bhk * s.S + key) * s.E;
 #pragma unroll
@@ -320,7 +375,7 @@ struct alignas(16) DqSmem {
     u32x4 v[2][T::SLOTS];
 };
 
-template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16>
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16, bool SPLIT = false>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32, NT = kQN / 32;
     __shared__ DqSmem<D> sm;
@@ -330,7 +385,12 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nqt = (s.L + kQM - 1) / kQM;
     const int w = logical_block();
-    const int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    int bh = w / nqt, qt = CAUSAL ? nqt - 1 - w % nqt : w % nqt;
+    // Split: blocks run over (head, query tile longest first, piece) (fwd_split.hpp).
+    int piece = 0, npieces = 1;
+    if constexpr (SPLIT) {
+        if (!split_block(s, kQM, kQN, a.chunk_q, w, &qt, &bh, &piece, &npieces)) return;
+    }
     const int b = bh / s.H, h = bh % s.H, hk = h / s.repeat;
     const int q0 = qt * kQM;
     const int qi = q0 + wave * 32 + lr;
@@ -380,17 +440,20 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
 
     const int kv_end = CAUSAL ? min(q0 + kQM, s.S) : s.S;
-    const int ntiles = (kv_end + kQN - 1) / kQN;
+    const int all_tiles = (kv_end + kQN - 1) / kQN;
+    // This block's key tiles [t_begin, ntiles): all of them, or its piece's.
+    const int t_begin = SPLIT ? piece * all_tiles / npieces : 0;
+    const int ntiles = SPLIT ? (piece + 1) * all_tiles / npieces : all_tiles;
     auto fill = [&](int t) {
         const int n0 = t * kQN, rows = min(kQN, s.S - n0);
         fill_cm<kQN, D, VEC, kQW>(sm.k[t & 1], kb + (int64_t)n0 * s.E, rows, s.E, wave, lane);
         fill_cm<kQN, D, VEC, kQW>(sm.v[t & 1], vb + (int64_t)n0 * s.E, rows, s.E, wave, lane);
     };
-    if (ntiles > 0) fill(0);
+    if (t_begin < ntiles) fill(t_begin);
     const uint32_t rowb = row_lanebase<kQN, D>(lane);
     const uint32_t trb = tr_lanebase<kQN, D>(lane);
 
-    for (int t = 0; t < ntiles; ++t) {
+    for (int t = t_begin; t < ntiles; ++t) {
         const int n0 = t * kQN;
         if (VEC) wait_vmem();
         __syncthreads();
@@ -475,6 +538,25 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
             for (int r = 0; r < 16; ++r) dq[dt][r] = ldexpf(dq[dt][r], -(fs.e_k + fs.e_pv - 24));
     }
+    if (SPLIT && npieces > 1) {
+        // A piece: its float32 partial goes to slot `piece` of the query's row
+        // (bwd_split_reduce_kernel sums them).
+        if (qi < s.L) {
+            const size_t nrows = (size_t)s.B * s.H * s.L;
+            float *pq = a.split + ((size_t)2 * a.max_k * s.B * s.Hkv * s.S * s.E) +
+                        ((size_t)piece * nrows + (int64_t)bh * s.L + qi) * s.E;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; r += 4) {
+                    const int d = dt * 32 + acc_row(r, g);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (d + u < s.E) pq[d + u] = dq[dt][r + u] * s.scale;
+                }
+        }
+        return;
+    }
     if (qi < s.L) {
         __bf16 *dqr = static_cast<__bf16 *>(a.dq) + ((int64_t)bh * s.L + qi) * s.E;
 #pragma unroll
@@ -495,6 +577,115 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                 }
             }
     }
+}
+
+// Sums the float32 partials of split rows in piece order into a bf16 output, one thread per 4
+// consecutive dims of a row: rows of dK and dV (`which` 0: key rows, key tile = row % S / kKN) or
+// of dQ (`which` 1: query rows, query tile = row % L / kQM).  Rows of tiles that ran whole were
+// written by their kernel and are skipped.
+__global__ __launch_bounds__(256) void bwd_split_reduce_kernel(BwdArgs a, int which) {
+    const AttnShape &s = a.s;
+    const int cpr = (s.E + 3) / 4;  // 4-dim groups per row
+    const int64_t nrows = which == 0 ? (int64_t)s.B * s.Hkv * s.S : (int64_t)s.B * s.H * s.L;
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= nrows * cpr) return;
+    const int64_t row = id / cpr;
+    const int d0 = (int)(id % cpr) * 4;
+    const int np = which == 0 ? dkdv_pieces(s, (int)(row % s.S) / kKN, a.chunk_k)
+                              : fwd_pieces(s, kQM, kQN, (int)(row % s.L) / kQM, a.chunk_q);
+    if (np <= 1) return;
+    const int nout = which == 0 ? 2 : 1;
+    const float *base = a.split + (which == 0 ? 0 : (size_t)2 * a.max_k * s.B * s.Hkv * s.S * s.E);
+    for (int o = 0; o < nout; ++o) {
+        const float *src = base + ((size_t)o * a.max_k * nrows + row) * s.E + d0;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < np; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (d0 + e < s.E) acc[e] += src[(size_t)p * nrows * s.E + e];
+        __bf16 *dst = static_cast<__bf16 *>(which == 1 ? a.dq : o == 0 ? a.dk : a.dv) + row * s.E + d0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (d0 + e < s.E) dst[e] = static_cast<__bf16>(acc[e]);
+    }
+}
+
+// The split of both backward grids on the current device (the fp16-copy path without a mask):
+// pieces of at least 4 steps (dK/dV) or 4 key tiles (dQ), no more pieces than resident
+// workgroups, only for grids that fill at most half of them.
+struct BwdSplitPlan {
+    int chunk_k = 0, max_k = 1, chunk_q = 0, max_q = 1;
+    int64_t blocks_k = 0, blocks_q = 0;
+    size_t bytes = 0;
+};
+
+template <int D>
+BwdSplitPlan plan_bwd(const AttnShape &s) {
+    BwdSplitPlan p;
+    if (s.mask != nullptr || s.L == 0 || s.S == 0) return p;
+    const int nkt = (s.S + kKN - 1) / kKN;
+    const int64_t BHk = (int64_t)s.B * s.Hkv;
+    const int64_t slots_k = split_slots(
+        reinterpret_cast<const void *>(&bwd_dkdv_bf16_kernel<D, true, false, true, true, true>), kKThreads, nkt * BHk);
+    if (slots_k > 0 && 2 * nkt * BHk <= slots_k) {
+        int64_t steps = 0;
+        int most = 0;
+        for (int kt = 0; kt < nkt; ++kt) {
+            const int n = dkdv_steps(s, kt);
+            steps += n;
+            most = n > most ? n : most;
+        }
+        int64_t chunk = (steps * BHk + slots_k - 1) / slots_k;
+        for (chunk = chunk < 4 ? 4 : chunk; chunk < most; ++chunk) {
+            p.blocks_k = 0;
+            for (int kt = 0; kt < nkt; ++kt) p.blocks_k += BHk * dkdv_pieces(s, kt, (int)chunk);
+            if (p.blocks_k <= slots_k) break;
+        }
+        if (chunk < most) {
+            p.chunk_k = (int)chunk;
+            for (int kt = 0; kt < nkt; ++kt) p.max_k = std::max(p.max_k, dkdv_pieces(s, kt, p.chunk_k));
+        }
+    }
+    const int64_t nqt = (s.L + kQM - 1) / kQM;
+    const int64_t slots_q = split_slots(
+        reinterpret_cast<const void *>(&bwd_dq_bf16_kernel<D, true, false, true, true, true>), kQThreads,
+        nqt * s.B * s.H);
+    const FwdSplitPlan q = plan_split(s, kQM, kQN, slots_q);
+    p.chunk_q = q.chunk, p.max_q = q.max_pieces, p.blocks_q = q.blocks;
+    const size_t kv_rows = p.chunk_k > 0 ? (size_t)2 * p.max_k * BHk * s.S : (size_t)2 * BHk * s.S;
+    const size_t q_rows = p.chunk_q > 0 ? (size_t)p.max_q * s.B * s.H * s.L : 0;
+    if (p.chunk_k > 0 || p.chunk_q > 0) p.bytes = (kv_rows + q_rows) * s.E * sizeof(float);
+    return p;
+}
+
+// The split grids and their reductions (the fp16-copy path without a mask).
+template <int D, bool VEC>
+hipError_t launch_split(const BwdArgs &args, const BwdSplitPlan &p, hipStream_t st) {
+    BwdArgs a = args;
+    a.chunk_k = p.chunk_k, a.max_k = p.max_k, a.chunk_q = p.chunk_q, a.max_q = p.max_q;
+    const bool causal = a.s.causal;
+    const dim3 bk(kKThreads), bq(kQThreads), br(256);
+    if (p.chunk_k > 0) {
+        const dim3 gk((unsigned)p.blocks_k);
+        if (causal) return_if(launch(bwd_dkdv_bf16_kernel<D, true, false, VEC, true, true>, gk, bk, st, a));
+        else return_if(launch(bwd_dkdv_bf16_kernel<D, false, false, VEC, true, true>, gk, bk, st, a));
+        const int64_t n = (int64_t)a.s.B * a.s.Hkv * a.s.S * ((a.s.E + 3) / 4);
+        return_if(launch(bwd_split_reduce_kernel, dim3((unsigned)((n + 255) / 256)), br, st, a, 0));
+    } else {
+        const dim3 gk(((a.s.S + kKN - 1) / kKN) * a.s.B * a.s.Hkv);
+        if (causal) return_if(launch(bwd_dkdv_bf16_kernel<D, true, false, VEC, true>, gk, bk, st, a));
+        else return_if(launch(bwd_dkdv_bf16_kernel<D, false, false, VEC, true>, gk, bk, st, a));
+    }
+    if (p.chunk_q > 0) {
+        const dim3 gq((unsigned)p.blocks_q);
+        if (causal) return_if(launch(bwd_dq_bf16_kernel<D, true, false, VEC, true, true>, gq, bq, st, a));
+        else return_if(launch(bwd_dq_bf16_kernel<D, false, false, VEC, true, true>, gq, bq, st, a));
+        const int64_t n = (int64_t)a.s.B * a.s.H * a.s.L * ((a.s.E + 3) / 4);
+        return launch(bwd_split_reduce_kernel, dim3((unsigned)((n + 255) / 256)), br, st, a, 1);
+    }
+    const dim3 gq(((a.s.L + kQM - 1) / kQM) * a.s.B * a.s.H);
+    if (causal) return launch(bwd_dq_bf16_kernel<D, true, false, VEC, true>, gq, bq, st, a);
+    return launch(bwd_dq_bf16_kernel<D, false, false, VEC, true>, gq, bq, st, a);
 }
 
 template <int D, bool VEC, bool F16>
@@ -530,6 +721,10 @@ hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     return_if(launch_to_f16(a.dout, a.do16, n, qslab, a.f16_partial, a.exps + 3 * n, st));
     BwdArgs f = a;
     f.q = a.q16, f.k = a.k16, f.v = a.v16, f.dout = a.do16;
+    if (a.split) {
+        const BwdSplitPlan p = plan_bwd<D>(a.s);
+        if ((p.chunk_k > 0 || p.chunk_q > 0) && p.bytes <= a.split_bytes) return launch_split<D, VEC>(f, p, st);
+    }
     return launch_dvf<D, VEC, true>(f, st);
 }
 
@@ -541,6 +736,13 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
 }
 
 }  // namespace
+
+size_t bwd_bf16_split_bytes(const AttnShape &s) {
+    if (s.B * s.Hkv == 0 || s.L == 0 || s.S == 0) return 0;
+    if (s.E <= 32) return plan_bwd<32>(s).bytes;
+    if (s.E <= 64) return plan_bwd<64>(s).bytes;
+    return plan_bwd<128>(s).bytes;
+}
 
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st) {
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;

@@ -59,6 +59,14 @@ struct BwdArgs {
     void *q16, *k16, *v16, *do16;
     float *f16_partial;
     int *exps;
+    // bf16 with the fp16 copies, no mask, grids that fill under half the device: the dK/dV
+    // kernel's key tiles run as pieces of at most chunk_k query steps and the dQ kernel's query
+    // tiles as pieces of at most chunk_q key tiles, each writing float32 partials (max_k / max_q
+    // slots per row) that a reduction sums in piece order into the bf16 outputs.  nullptr: no
+    // split.
+    float *split;
+    size_t split_bytes;
+    int chunk_k, max_k, chunk_q, max_q;
 };
 
 struct DecodeArgs {
@@ -97,6 +105,9 @@ hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st);
 size_t fwd_bf16_split_bytes(const AttnShape &s);
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);
+// Workspace bytes the bf16 backward uses to split its grids on the current device (0: it does not
+// split this shape).
+size_t bwd_bf16_split_bytes(const AttnShape &s);
 hipError_t launch_decode(const DecodeArgs &a, bool bf16, hipStream_t st);
 int decode_splits(const AttnShape &s, int *split_len);
 // `vec`: rows (and mask rows) start 16-byte aligned and the width is a multiple of 4.

@@ -80,7 +80,9 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
 /* Backward (dq, dk, dv) from the saved out and lse.  src/lib.rs:640-683,
  * src/torch_attention.rs:286-468.  The workspace must hold dsum (batch * heads * q_len floats);
  * the size returned also covers, for bf16, scaled fp16 copies of q, k, v and grad_out (with
- * less, P and dS enter their products as bf16 hi + lo pairs). */
+ * less, P and dS enter their products as bf16 hi + lo pairs) and, for bf16 without a mask on
+ * grids that fill at most half of the current device, the float32 partials of its split grids
+ * (so the size depends on the device current at the call). */
 size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q, const void *k,
                       const void *v, const void *out, const float *lse, const float *mask,

@@ -7,7 +7,11 @@ each writing a normalized partial output and lse, merged by a second kernel (row
 that ran whole are written directly).  The cases below take that path on MI355X; out and lse
 start as NaN, so a row neither path writes fails.
 
-Backward: the backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
+Backward (bf16, with its fp16 copies): on grids that fill at most half of the device, the dK/dV
+kernel's key tiles run as pieces over their query steps and the dQ kernel's query tiles as pieces
+over their key tiles, each piece writing float32 partials that a reduction sums in piece order.
+
+Backward (float32): the backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
 whole tiles would leave part of the device idle (fewer tiles than resident workgroups, or a
 ragged last wave of equal non-causal tiles), cuts the steps of all tiles into equal ranges, one
 per resident workgroup (stream-K).  A tile cut between ranges adds its dK / dV atomically into rows the pre-kernel
@@ -97,6 +101,46 @@ def test_bf16_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
     out, lse = _forward_nan_filled(q, k, v, causal, torch.bfloat16)
     assert_bf16(out, ref_o, f"{tag} out")
     assert_bf16(lse, ref_l, f"{tag} lse")
+
+
+BF16_BWD_CASES = [  # tag, B, H, Hkv, L, S, E, causal
+    ("causal_e128", 1, 2, 2, 2048, 2048, 128, True),
+    ("full_e64", 1, 1, 1, 4096, 4096, 64, False),
+    ("grouped_e128", 1, 4, 2, 1024, 1024, 128, True),
+    ("causal_s_gt_l", 1, 2, 2, 700, 1500, 64, True),   # key tiles past L have no steps
+    ("causal_l_gt_s", 1, 2, 2, 1500, 600, 128, True),
+    ("causal_e32", 2, 1, 1, 1536, 1536, 32, True),
+    ("unaligned_e40", 1, 1, 1, 700, 900, 40, False),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal", BF16_BWD_CASES, ids=[c[0] for c in BF16_BWD_CASES])
+def test_bf16_backward_split_grids(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
+    """The bf16 backward's split grids (dK/dV pieces over query steps, dQ pieces over key tiles,
+    float32 partials summed in piece order) against the oracle's backward from the GPU's own bf16
+    out and lse, to the bf16 bar; dq, dk, dv start as NaN."""
+    from densecore_amd import _lib, _native
+    rng = np.random.default_rng(sum(map(ord, tag)) + 3)
+    q, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(2))
+    k, v = (bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32)) for _ in range(2))
+    print(f"[case] bf16 backward split {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
+    tq, tk, tv, tg = (_t(x).to(torch.bfloat16) for x in (q, k, v, g))
+    out, lse = _native._flash_attention(tq, tk, tv, causal)
+    torch.cuda.synchronize()
+    ref = oracle_lib.backward(g, q, k, v, out.float().cpu().numpy(), lse.cpu().numpy(), causal)
+    dims = _native._attention_dims(tq, tk, tv)
+    dq = torch.full((B, H, L, E), float("nan"), device=DEV, dtype=torch.bfloat16)
+    dk = torch.full((B, Hkv, S, E), float("nan"), device=DEV, dtype=torch.bfloat16)
+    dv = torch.full((B, Hkv, S, E), float("nan"), device=DEV, dtype=torch.bfloat16)
+    d = _native._desc(dims, causal, None, torch.bfloat16, (0, 0, 0))
+    L_ = _lib.lib()
+    ws = _native._workspace(L_.dc_sdpa_bwd_workspace_size(d), tq.device)
+    _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(tg), _native._ptr(tq), _native._ptr(tk), _native._ptr(tv),
+                              _native._ptr(out), _native._ptr(lse), None, _native._ptr(dq), _native._ptr(dk),
+                              _native._ptr(dv), _native._ptr(ws), ws.numel(), _native._stream(tq.device)))
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        assert_bf16(a.float().cpu().numpy(), b, f"{tag} {name}")
 
 
 def _backward_nan_filled(g, q, k, v, out, lse, causal, mask=None):
