@@ -1,6 +1,6 @@
 """Benchmark of the SDPA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only C2,C4,math]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only C2,C4,math,sched]
 
 A step is one pass of the hot path over one batch of synthetic, HBM-resident input:
 C2 (the headline) is causal fp32 forward + backward at B8 H12 T1024
@@ -11,7 +11,8 @@ throughput (wall clock over K steps between two synchronizations), a roofline en
 entry point whose kernel time comes from HIP events on the launch stream around back-to-back
 calls of that entry point alone, and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
 ``math_path`` reports the composed path's own kernels (softmax forward/backward, the Bernoulli
-mask from the reference's generator stream, the dropout product) at C3's shape.
+mask from the reference's generator stream, the dropout product) at C3's shape.  ``--only sched``
+(not in the default run) times the few-heads shapes that take the split / stream-K schedules.
 """
 import argparse
 import json
@@ -263,13 +264,48 @@ def cpu_baseline(threads):
             "configs": per}
 
 
+# Shapes whose whole-tile grids fill little of the device (few heads, long rows), where the
+# alternative schedules run: the split forward (float32, bf16), the float32 backward's stream-K
+# ranges and the bf16 backward's split grids.  Not part of the default run (--only sched).
+SCHED_SHAPES = [  # B, H, L, E, causal, dtype
+    (1, 8, 2048, 64, True, "f32"), (1, 4, 4096, 64, True, "f32"), (1, 8, 2048, 128, True, "f32"),
+    (8, 12, 512, 64, True, "f32"), (6, 16, 1024, 64, False, "f32"),
+    (1, 1, 16384, 128, True, "bf16"), (1, 2, 8192, 128, True, "bf16"), (1, 4, 4096, 128, True, "bf16"),
+]
+
+
+def bench_schedules(torch, native, steps, dev):
+    """Kernel time per call (HIP events around back-to-back calls) of dc_sdpa_fwd and dc_sdpa_bwd
+    on SCHED_SHAPES, synthetic N(0, 1) inputs."""
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    n = max(steps, 10)
+    for B, H, L, E, causal, dtn in SCHED_SHAPES:
+        dt = torch.bfloat16 if dtn == "bf16" else torch.float32
+        q, k, v, g = (torch.randn(B, H, L, E, device=dev, generator=gen).to(dt) for _ in range(4))
+        o, lse = native._flash_attention(q, k, v, causal)
+        for _ in range(3):
+            native._flash_attention(q, k, v, causal)
+            native._flash_attention_backward(g, q, k, v, o, lse, causal)
+        fms = kernel_ms(torch, stream, lambda: native._flash_attention(q, k, v, causal), n)
+        bms = kernel_ms(torch, stream, lambda: native._flash_attention_backward(g, q, k, v, o, lse, causal), n)
+        ff, fb = flops(B, H, L, L, E, causal, True)
+        out[f"{dtn} B{B} H{H} L{L} D{E} {'causal' if causal else 'full'}"] = {
+            "fwd_ms": round(fms, 4), "bwd_ms": round(bms, 4),
+            "fwd_tflops": round(ff / (fms * 1e-3) / 1e12, 1), "bwd_tflops": round(fb / (bms * 1e-3) / 1e12, 1)}
+        del q, k, v, g, o, lse
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of configs to run (C1..C5, math)")
+    ap.add_argument("--only", default="", help="comma list of configs to run (C1..C5, math, sched)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (torch copy_), the kernel "
                          "of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -309,6 +345,8 @@ def main():
     if "math" in only or not args.only:
         results["math"] = bench_math(torch, args.steps, args.warmup, dev)
         torch.cuda.empty_cache()
+    if "sched" in only:
+        results["sched"] = bench_schedules(torch, native, args.steps, dev)
 
     traffic = load_traffic()
     line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -359,6 +397,8 @@ def main():
         line["other_configs"] = others
     if results.get("math"):
         line["math_path"] = results["math"]
+    if results.get("sched"):
+        line["schedules"] = results["sched"]
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         line["cpu_baseline"] = cpu_baseline(threads)
