@@ -92,7 +92,7 @@ dc_status launched(hipError_t e) {
 size_t fwd_order_ws(const dc::AttnShape &s) { return round_up((size_t)2 * s.B * s.H * sizeof(int)); }
 size_t fwd_v16_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * s.S * s.E * 2); }
 size_t fwd_partial_ws(const dc::AttnShape &s) {
-    return round_up((size_t)s.B * s.Hkv * dc::f16_parts((int64_t)s.S * s.E) * sizeof(float));
+    return round_up((size_t)s.B * s.Hkv * dc::f16_parts((int64_t)s.B * s.Hkv, (int64_t)s.S * s.E) * sizeof(float));
 }
 size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
@@ -120,7 +120,8 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     if (bf16) {
         const size_t nq = (size_t)s.B * s.H * s.L * s.E, nk = (size_t)s.B * s.Hkv * s.S * s.E;
         const int64_t qslab = (int64_t)s.repeat * s.L * s.E, kslab = (int64_t)s.S * s.E;
-        const int parts = std::max(dc::f16_parts(qslab), dc::f16_parts(kslab));
+        const int64_t nslabs = (int64_t)s.B * s.Hkv;
+        const int parts = std::max(dc::f16_parts(nslabs, qslab), dc::f16_parts(nslabs, kslab));
         l.q16 = take(nq * 2);
         l.do16 = take(nq * 2);
         l.k16 = take(nk * 2);

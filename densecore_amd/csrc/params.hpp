@@ -91,7 +91,7 @@ struct SoftmaxArgs {
 };
 
 // bf16 -> fp16 copies scaled per slab (f16_stage.hip): segments per slab, and the two passes.
-int f16_parts(int64_t slab);
+int f16_parts(int64_t nslabs, int64_t slab);
 hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t slab, float *partial, int *exps,
                          hipStream_t st);
 
