@@ -596,13 +596,19 @@ __global__ __launch_bounds__(256) void bwd_split_reduce_kernel(BwdArgs a, int wh
     if (np <= 1) return;
     const int nout = which == 0 ? 2 : 1;
     const float *base = a.split + (which == 0 ? 0 : (size_t)2 * a.max_k * s.B * s.Hkv * s.S * s.E);
+    const bool vec = (s.E & 3) == 0;  // partial rows 16-byte aligned (the workspace is)
     for (int o = 0; o < nout; ++o) {
         const float *src = base + ((size_t)o * a.max_k * nrows + row) * s.E + d0;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int p = 0; p < np; ++p)
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (vec) {
+#pragma unroll 4
+            for (int p = 0; p < np; ++p) acc += *reinterpret_cast<const f32x4 *>(src + (size_t)p * nrows * s.E);
+        } else {
+            for (int p = 0; p < np; ++p)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (d0 + e < s.E) acc[e] += src[(size_t)p * nrows * s.E + e];
+                for (int e = 0; e < 4; ++e)
+                    if (d0 + e < s.E) acc[e] += src[(size_t)p * nrows * s.E + e];
+        }
         __bf16 *dst = static_cast<__bf16 *>(which == 1 ? a.dq : o == 0 ? a.dk : a.dv) + row * s.E + d0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)

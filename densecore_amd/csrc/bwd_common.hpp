@@ -19,7 +19,19 @@ DEVI void bwd_pre_block(const BwdArgs &a, int64_t block) {
     const T *go = static_cast<const T *>(a.dout) + row * s.E;
     const T *o = static_cast<const T *>(a.out) + row * s.E;
     float acc = 0.f;
-    for (int d = part; d < s.E; d += 16) acc = fmaf(to_f32<T>(go[d]), to_f32<T>(o[d]), acc);
+    // 16-byte chunks per lane when rows are whole chunks on 16-byte boundaries.
+    constexpr int VW = 16 / sizeof(T);
+    typedef T tvec __attribute__((ext_vector_type(VW)));
+    if (s.E % VW == 0 && ((reinterpret_cast<uintptr_t>(a.dout) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0) {
+        for (int c = part; c < s.E / VW; c += 16) {
+            const tvec x = *reinterpret_cast<const tvec *>(go + c * VW);
+            const tvec y = *reinterpret_cast<const tvec *>(o + c * VW);
+#pragma unroll
+            for (int e = 0; e < VW; ++e) acc = fmaf(to_f32<T>(x[e]), to_f32<T>(y[e]), acc);
+        }
+    } else {
+        for (int d = part; d < s.E; d += 16) acc = fmaf(to_f32<T>(go[d]), to_f32<T>(o[d]), acc);
+    }
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
     if (part == 0) a.dsum[row] = acc;

@@ -45,6 +45,7 @@ __global__ __launch_bounds__(kThreads) void slab_max_kernel(const uint16_t *src,
     const uint16_t *x = src + (int64_t)s * slab;
     float m = 0.f;
     if (vec) {  // segments start at multiples of 8 elements (slab % 8 == 0, per % 8 == 0)
+#pragma unroll 4
         for (int64_t i = i0 + 8 * threadIdx.x; i < i1; i += 8 * kThreads) {
             const u16x8 v = *reinterpret_cast<const u16x8 *>(x + i);
 #pragma unroll
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(kThreads) void slab_convert_kernel(const uint16_t *
         return static_cast<_Float16>(ldexpf(__uint_as_float((uint32_t)bits << 16), e));
     };
     if (vec) {
+#pragma unroll 4
         for (int64_t i = i0 + 8 * threadIdx.x; i < i1; i += 8 * kThreads) {
             const u16x8 v = *reinterpret_cast<const u16x8 *>(x + i);
             f16x8 o;
