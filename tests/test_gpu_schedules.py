@@ -196,3 +196,53 @@ def test_backward_schedules(oracle_lib, tag, B, H, Hkv, L, S, E, causal, mask):
     assert_f32(dq, rq, f"{tag} dq")
     assert_f32(dk, rk, f"{tag} dk")
     assert_f32(dv, rv, f"{tag} dv")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_split_shapes_without_split_workspace(oracle_lib, dtype):
+    """Shapes that split when given the full workspace, run with less: the forward with none at
+    all (whole query tiles, and for bf16 the hi + lo P V product), the backward with the float32
+    minimum (dsum only) or, for bf16, exactly the fp16 copies without the split partials (the
+    whole-tile grids).  Results still meet the bar."""
+    from densecore_amd import _lib, _native
+    B, H, L, E, causal = 1, 2, 1536, 128, True
+    bf16 = dtype == "bf16"
+    rng = np.random.default_rng(77 if bf16 else 78)
+    q, k, v, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(4))
+    if bf16:
+        q, k, v, g = (bf16_round(x) for x in (q, k, v, g))
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tq, tk, tv, tg = (_t(x).to(dt) for x in (q, k, v, g))
+    dims = _native._attention_dims(tq, tk, tv)
+    d = _native._desc(dims, causal, None, dt, (0, 0, 0))
+    L_ = _lib.lib()
+    stream = _native._stream(tq.device)
+    print(f"[case] reduced workspaces {dtype} B{B} H{H} L{L} E{E}", flush=True)
+    assert L_.dc_sdpa_fwd_workspace_size(d) > 256  # the full size holds split partials
+    out = torch.full((B, H, L, E), float("nan"), device=DEV, dtype=dt)
+    lse = torch.full((B, H, L), float("nan"), device=DEV)
+    _lib.check(L_.dc_sdpa_fwd(d, _native._ptr(tq), _native._ptr(tk), _native._ptr(tv), None, _native._ptr(out),
+                              _native._ptr(lse), None, 0, stream))
+    torch.cuda.synchronize()
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    check = assert_bf16 if bf16 else assert_f32
+    check(out.float().cpu().numpy(), ref_o, f"{dtype} out, no workspace")
+    check(lse.cpu().numpy(), ref_l, f"{dtype} lse, no workspace")
+    full = L_.dc_sdpa_bwd_workspace_size(d)
+    # bf16: dsum + the fp16 copies = the full size minus the split partials; float32: dsum only.
+    dsum_bytes = (B * H * L * 4 + 255) // 256 * 256
+    less = full - 1 if bf16 else dsum_bytes
+    ws = _native._workspace(less, tq.device)
+    dq, dk, dv = (torch.full((B, H, L, E), float("nan"), device=DEV, dtype=dt) for _ in range(3))
+    o_in = out if bf16 else _t(ref_o)
+    l_in = lse if bf16 else torch.from_numpy(ref_l).to(DEV)
+    _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(tg), _native._ptr(tq), _native._ptr(tk), _native._ptr(tv),
+                              _native._ptr(o_in), _native._ptr(l_in), None, _native._ptr(dq), _native._ptr(dk),
+                              _native._ptr(dv), _native._ptr(ws), less, stream))
+    torch.cuda.synchronize()
+    if bf16:
+        ref = oracle_lib.backward(g, q, k, v, out.float().cpu().numpy(), lse.cpu().numpy(), causal)
+    else:
+        ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal)
+    for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        check(a.float().cpu().numpy(), b, f"{dtype} {name}, reduced workspace")
