@@ -17,6 +17,7 @@ EXPORTS = ("dc_abi_version", "dc_last_error",
            "dc_sdpa_fwd_workspace_size", "dc_sdpa_fwd",
            "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
            "dc_sdpa_decode_workspace_size", "dc_sdpa_decode",
+           "dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule",
            "dc_softmax_fwd", "dc_softmax_bwd",
            "dc_mt19937_seed", "dc_mt19937_advance", "dc_mt19937_table_bytes",
            "dc_mt19937_table_init", "dc_bernoulli_max_draws", "dc_bernoulli_workspace_size",
@@ -31,6 +32,18 @@ class Desc(ctypes.Structure):
                 ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("mask_stride_b", ctypes.c_int64), ("mask_stride_h", ctypes.c_int64),
                 ("mask_stride_l", ctypes.c_int64)]
+
+
+class Schedule(ctypes.Structure):
+    """``dc_sdpa_schedule``."""
+    _fields_ = [("split_chunk", ctypes.c_int32), ("split_pieces", ctypes.c_int32),
+                ("streamk_ranges", ctypes.c_int32), ("split_chunk_k", ctypes.c_int32),
+                ("split_chunk_q", ctypes.c_int32), ("f16_products", ctypes.c_int32),
+                ("deterministic", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("workgroups", ctypes.c_int64)]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
 
 
 class SoftmaxDesc(ctypes.Structure):
@@ -62,6 +75,9 @@ def lib():
         L.dc_sdpa_fwd.argtypes = [D, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_bwd.argtypes = [D, P, P, P, P, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_decode.argtypes = [D, P, P, P, P, P, P, SZ, P]
+        for name in ("dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule"):
+            getattr(L, name).argtypes = [D, ctypes.c_int, SZ, ctypes.POINTER(Schedule)]
+            getattr(L, name).restype = ctypes.c_int
         SD = ctypes.POINTER(SoftmaxDesc)
         L.dc_softmax_fwd.argtypes = [SD, P, P, P, P]
         L.dc_softmax_bwd.argtypes = [SD, P, P, P, P]

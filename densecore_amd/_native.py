@@ -75,8 +75,36 @@ def _stream(dev):
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+# One workspace per (device, stream), grown on demand and reused: calls on one stream run in
+# order, so a call never overlaps the previous user of its stream's workspace.
+_WORKSPACES = {}
+
+
 def _workspace(nbytes, dev):
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    nbytes = max(int(nbytes), 1)
+    key = (dev.index, _stream(dev))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _schedule(backward, q, k, v, causal, scale=None, mask=None, workspace_bytes=None):
+    """The schedule ``dc_sdpa_fwd`` (or ``dc_sdpa_bwd``) takes for these arguments on the current
+    device, with the workspace ``_flash_attention`` passes (or ``workspace_bytes``)."""
+    dims = _attention_dims(q, k, v)
+    _, dtype = _check_device(q, k, v)
+    ms = _mask_arg(mask, dims, q.device)[1] if mask is not None else (0, 0, 0)
+    d = _desc(dims, causal, scale, dtype, ms)
+    L_ = _lib.lib()
+    if workspace_bytes is None:
+        size = L_.dc_sdpa_bwd_workspace_size if backward else L_.dc_sdpa_fwd_workspace_size
+        workspace_bytes = max(int(size(d)), 1)
+    out = _lib.Schedule()
+    query = L_.dc_sdpa_bwd_schedule if backward else L_.dc_sdpa_fwd_schedule
+    _lib.check(query(d, int(mask is not None), int(workspace_bytes), out))
+    return out.as_dict()
 
 
 def _flash_attention(q, k, v, causal, scale=None, mask=None):

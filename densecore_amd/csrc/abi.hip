@@ -6,13 +6,58 @@
 // reference's ValueError text.  Launch failures return DC_EXECUTION_FAILED (the reference's
 // RuntimeError, src/lib.rs:633, 677).
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 
+#include "common.hpp"
 #include "dc_attn.h"
 #include "dc_math.h"
 #include "params.hpp"
+
+namespace dc {
+namespace {
+// Per-device facts the launchers consult on every call (grid sizing), looked up once.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+std::mutex g_occupancy_mutex;
+std::map<std::tuple<int, const void *, int>, int> g_occupancy;
+}  // namespace
+
+int device_cus() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < kMaxDevices) {
+        const int c = g_cus[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < kMaxDevices && cus > 0) g_cus[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+int device_occupancy(const void *kernel, int threads) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    const auto key = std::make_tuple(dev, kernel, threads);
+    {
+        std::lock_guard<std::mutex> lock(g_occupancy_mutex);
+        const auto it = g_occupancy.find(key);
+        if (it != g_occupancy.end()) return it->second;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(g_occupancy_mutex);
+    g_occupancy[key] = per_cu;
+    return per_cu;
+}
+
+}  // namespace dc
 
 namespace {
 
@@ -308,6 +353,54 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     hipStream_t strm = static_cast<hipStream_t>(stream);
     if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
     return launched(dc::launch_bwd_bf16(a, strm));
+}
+
+}  // extern "C"
+
+namespace {
+
+// Runs `call` (a dc_sdpa_* entry point over stand-in addresses) as a dry run and reports the
+// schedule its launchers chose.  Nothing is launched, so the addresses are never dereferenced.
+template <typename F>
+dc_status dry_run(dc_sdpa_schedule *out, F call) {
+    if (out == nullptr) return fail(DC_INVALID_ARGUMENT, "flash attention schedule output is null");
+    dc::Schedule sch;
+    dc::g_schedule = &sch;
+    const dc_status st = call(reinterpret_cast<void *>(uintptr_t{1} << 12));
+    dc::g_schedule = nullptr;
+    if (st != DC_OK) return st;
+    *out = dc_sdpa_schedule{};
+    out->split_chunk = sch.split_chunk;
+    out->split_pieces = sch.split_pieces;
+    out->streamk_ranges = sch.streamk_ranges;
+    out->split_chunk_k = sch.split_chunk_k;
+    out->split_chunk_q = sch.split_chunk_q;
+    out->f16_products = sch.f16_products;
+    out->deterministic = sch.deterministic;
+    out->workgroups = sch.workgroups;
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+dc_status dc_sdpa_fwd_schedule(const dc_attn_desc *d, int has_mask, size_t workspace_bytes,
+                               dc_sdpa_schedule *out) {
+    return dry_run(out, [&](void *p) {
+        return dc_sdpa_fwd(d, p, p, p, has_mask ? static_cast<const float *>(p) : nullptr, p,
+                           static_cast<float *>(p), workspace_bytes ? p : nullptr, workspace_bytes,
+                           nullptr);
+    });
+}
+
+dc_status dc_sdpa_bwd_schedule(const dc_attn_desc *d, int has_mask, size_t workspace_bytes,
+                               dc_sdpa_schedule *out) {
+    return dry_run(out, [&](void *p) {
+        return dc_sdpa_bwd(d, p, p, p, p, p, static_cast<const float *>(p),
+                           has_mask ? static_cast<const float *>(p) : nullptr, p, p, p,
+                           workspace_bytes ? p : nullptr, workspace_bytes, nullptr);
+    });
 }
 
 size_t dc_sdpa_decode_workspace_size(const dc_attn_desc *d) {

@@ -719,6 +719,7 @@ hipError_t launch_dvf(const BwdArgs &a, hipStream_t st) {
 template <int D, bool VEC>
 hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     if (!a.q16) return launch_dvf<D, VEC, false>(a, st);
+    record_schedule(f16_products, 1);
     const int64_t n = (int64_t)a.s.B * a.s.Hkv;
     const int64_t qslab = (int64_t)a.s.repeat * a.s.L * a.s.E, kslab = (int64_t)a.s.S * a.s.E;
     return_if(launch_to_f16(a.q, a.q16, n, qslab, a.f16_partial, a.exps, st));
@@ -729,7 +730,11 @@ hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     f.q = a.q16, f.k = a.k16, f.v = a.v16, f.dout = a.do16;
     if (a.split) {
         const BwdSplitPlan p = plan_bwd<D>(a.s);
-        if ((p.chunk_k > 0 || p.chunk_q > 0) && p.bytes <= a.split_bytes) return launch_split<D, VEC>(f, p, st);
+        if ((p.chunk_k > 0 || p.chunk_q > 0) && p.bytes <= a.split_bytes) {
+            record_schedule(split_chunk_k, p.chunk_k);
+            record_schedule(split_chunk_q, p.chunk_q);
+            return launch_split<D, VEC>(f, p, st);
+        }
     }
     return launch_dvf<D, VEC, true>(f, st);
 }

@@ -465,13 +465,7 @@ __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(BwdArgs a, StreamK sk,
 
 // Workgroups of the backward that fit on the device at once (the occupancy the kernel's
 // waves_per_eu attribute sets: two per CU at D <= 64 without a mask, one otherwise); 0 if unknown.
-int resident_workgroups(int D, bool mask) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    return cus * (D <= 64 && !mask ? 2 : 1);
-}
+int resident_workgroups(int D, bool mask) { return device_cus() * (D <= 64 && !mask ? 2 : 1); }
 
 // The stream-K schedule where whole tiles leave part of the device idle (measured on one MI355X,
 // dc_sdpa_bwd per call, whole tiles -> stream-K):
@@ -522,6 +516,8 @@ hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
     BwdArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked 16-byte alignment; E must fill D
     const StreamK sk = plan_streamk(a.s, D);
+    record_schedule(streamk_ranges, sk.chunks);
+    record_schedule(deterministic, 0);  // dQ (and cut tiles' dK / dV) by float atomics
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
     const int rows_blocks = (int)((rows + 15) / 16);
     const int64_t zero_blocks = sk.chunks > 0 ? (int64_t)a.s.B * a.s.Hkv * ((a.s.S + kBN - 1) / kBN) : 0;

@@ -106,11 +106,21 @@ template <> DEVI __bf16 from_f32<__bf16>(float x) { return static_cast<__bf16>(x
 // the compiler's wait-count pass does not treat the transfer as aliasing every later LDS read,
 // which would make each tile wait for the next tile's loads; the caller waits (vmcnt(0) +
 // barrier) before reading a filled buffer.
+//
+// The instruction takes its LDS address from m0, a register the compiler reserves (and may hold
+// live values in).  So the assembly saves m0 into an SGPR of its own, sets it, and restores it
+// after the load has issued (m0 is read at issue): the compiler's view of m0 is never changed,
+// and m0 need not be declared clobbered.  GFX9 parts need one wait state between an SALU write
+// of m0 and an LDS-DMA instruction that reads it (the s_nop).
 DEVI void lds_dma16(const void *src, void *dst) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base), "v"(src)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(base), "v"(src)
+                 : "memory");
 }
 
 // The same transfer addressed as a wave-uniform 64-bit base (held in SGPRs) plus a per-lane
@@ -125,8 +135,12 @@ DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
     const uint64_t sbase = ((uint64_t)hi << 32) | lo;
     const uint32_t m = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m), "v"(off), "s"(sbase)
-                 : "memory", "m0");
+    uint32_t saved;  // m0 saved and restored as in lds_dma16
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(m), "v"(off), "s"(sbase)
+                 : "memory");
 }
 
 // s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
@@ -146,15 +160,37 @@ DEVI void sched_reads_ahead() {
     __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
 }
 
+// The schedule a launcher chose (dc_sdpa_schedule of dc_attn.h).  While g_schedule is set on a
+// thread, launchers record their choices there and launch() starts nothing (a dry run: the
+// schedule query runs the very code that decides a launch).
+struct Schedule {
+    int split_chunk = 0, split_pieces = 1;  // forward split key ranges
+    int streamk_ranges = 0;                 // float32 backward
+    int split_chunk_k = 0, split_chunk_q = 0;  // bf16 backward split grids
+    int f16_products = 0;                   // bf16 products on the fp16 copies
+    int deterministic = 1;                  // backward results identical from run to run
+    int64_t workgroups = 0;                 // workgroups of the launches, summed
+};
+inline thread_local Schedule *g_schedule = nullptr;
+
 // Launches `kernel` and returns the status of this launch alone (hipGetLastError would also
 // report errors left behind by unrelated earlier calls in the process).
 template <typename... Params, typename... Args>
 inline hipError_t launch(void (*kernel)(Params...), dim3 grid, dim3 block, hipStream_t stream,
                          Args... args) {
     static_assert(sizeof...(Params) == sizeof...(Args), "argument count");
+    if (g_schedule) {
+        g_schedule->workgroups += (int64_t)grid.x * grid.y * grid.z;
+        return hipSuccess;
+    }
     void *ptrs[] = {static_cast<void *>(&args)...};
     return hipLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, 0, stream);
 }
+// Records a choice of the launcher when a dry run asks for it.
+#define record_schedule(field, value)                  \
+    do {                                               \
+        if (::dc::g_schedule) ::dc::g_schedule->field = (value); \
+    } while (0)
 
 #define return_if(expr)                      \
     do {                                     \

@@ -560,6 +560,7 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
         const int nqt = (a.s.L + kPPM - 1) / kPPM;
         const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
         if (a.v16) {
+            record_schedule(f16_products, 1);
             FwdArgs f = a;
             return_if(launch_to_f16(a.v, a.v16, (int64_t)a.s.B * a.s.Hkv, (int64_t)a.s.S * a.s.E,
                                     a.f16_partial, a.vexp, st));
@@ -567,6 +568,8 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
             if (a.split_o) {
                 const FwdSplitPlan p = plan<D>(a.s);
                 if (p.chunk > 0 && p.bytes <= a.split_bytes) {
+                    record_schedule(split_chunk, p.chunk);
+                    record_schedule(split_pieces, p.max_pieces);
                     f.split_chunk = p.chunk, f.split_max = p.max_pieces;
                     f.split_lse = f.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
                     const dim3 sgrid((unsigned)p.blocks);

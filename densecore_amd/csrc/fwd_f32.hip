@@ -481,6 +481,8 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
     if (a.split_o) {
         const FwdSplitPlan p = plan<D, BN, W>(a.s);
         if (p.chunk > 0 && p.bytes <= a.split_bytes) {
+            record_schedule(split_chunk, p.chunk);
+            record_schedule(split_pieces, p.max_pieces);
             a.split_chunk = p.chunk, a.split_max = p.max_pieces;
             a.split_lse = a.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
             const dim3 sgrid((unsigned)p.blocks);

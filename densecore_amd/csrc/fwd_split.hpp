@@ -33,13 +33,9 @@ struct FwdSplitPlan {
 // unknown or when a grid of `blocks` workgroups certainly fills more than half of them (no CU
 // holds more than 8 workgroups of these kernels).
 inline int64_t split_slots(const void *kernel, int threads, int64_t blocks) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    if (2 * blocks > 8 * (int64_t)cus) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) return 0;
-    return (int64_t)cus * per_cu;
+    const int cus = device_cus();
+    if (cus <= 0 || 2 * blocks > 8 * (int64_t)cus) return 0;
+    return (int64_t)cus * device_occupancy(kernel, threads);
 }
 
 // The split for a grid of query tiles of kBM queries over key tiles of BN keys, `slots`

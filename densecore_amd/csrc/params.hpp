@@ -90,6 +90,11 @@ struct SoftmaxArgs {
     bool safe;
 };
 
+// Compute units of the current device, and workgroups of `kernel` (`threads` per workgroup) that
+// fit on one of them; both looked up once per device (and kernel) and cached.  0 if unknown.
+int device_cus();
+int device_occupancy(const void *kernel, int threads);
+
 // bf16 -> fp16 copies scaled per slab (f16_stage.hip): segments per slab, and the two passes.
 int f16_parts(int64_t nslabs, int64_t slab);
 hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t slab, float *partial, int *exps,

@@ -30,8 +30,10 @@
  * All pointers are device pointers (hipMalloc'd or equivalent).  Calls are asynchronous and
  * ordered on `stream` (a hipStream_t; NULL is the null stream).  The caller owns every buffer;
  * workspaces are sized by the matching *_workspace_size call and must be 256-byte aligned.
- * The library's only global state is the thread-local last error and, once the generator of
- * dc_math.h is first used, its jump-ahead polynomials (built once, read-only after).
+ * The library's global state: the thread-local last error, per-device caches of facts the
+ * launchers size grids by (compute-unit count, kernel occupancy; looked up once, read-only
+ * after), and, once the generator of dc_math.h is first used, its jump-ahead polynomials (built
+ * once, read-only after).
  */
 #ifndef DC_ATTN_H
 #define DC_ATTN_H
@@ -98,6 +100,28 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
 
 /* Message of the last non-DC_OK status on the calling thread ("" if none). */
 const char *dc_last_error(void);
+
+/* The schedule dc_sdpa_fwd / dc_sdpa_bwd would run for a descriptor on the current device, given
+ * whether a mask is passed and the workspace size.  No counterpart in the reference (whose
+ * schedule is fixed, src/torch_attention.rs:14-35, 107-128): it lets a caller (and the tests)
+ * see which grid a call takes.  The query runs the launchers' own decision code without launching
+ * anything and touches no device memory. */
+typedef struct {
+    int32_t split_chunk;    /* forward: key tiles per piece of a split query tile; 0: no split */
+    int32_t split_pieces;   /* forward: most pieces of one query tile (1 without a split) */
+    int32_t streamk_ranges; /* float32 backward: stream-K ranges; 0: one workgroup per key tile */
+    int32_t split_chunk_k;  /* bf16 backward: query steps per dK/dV piece; 0: whole key tiles */
+    int32_t split_chunk_q;  /* bf16 backward: key tiles per dQ piece; 0: whole query tiles */
+    int32_t f16_products;   /* bf16: 1 when the products run on the scaled fp16 copies */
+    int32_t deterministic;  /* backward: 1 when dq, dk, dv are identical from run to run */
+    int32_t reserved;
+    int64_t workgroups;     /* workgroups of all the call's launches */
+} dc_sdpa_schedule;
+
+dc_status dc_sdpa_fwd_schedule(const dc_attn_desc *d, int has_mask, size_t workspace_bytes,
+                               dc_sdpa_schedule *out);
+dc_status dc_sdpa_bwd_schedule(const dc_attn_desc *d, int has_mask, size_t workspace_bytes,
+                               dc_sdpa_schedule *out);
 
 #ifdef __cplusplus
 }

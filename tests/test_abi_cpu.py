@@ -169,3 +169,38 @@ def test_decode_workspace_covers_splits():
         # per split
         splits = max(1, -(-S // 2048))
         assert ws >= B * H * splits * (E + 2) * 4
+
+
+def test_schedule_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "dc_attn.h"\n'
+                   "int main(void){printf(\"%zu %zu %zu\\n\", sizeof(dc_sdpa_schedule),"
+                   " offsetof(dc_sdpa_schedule, deterministic), offsetof(dc_sdpa_schedule, workgroups));"
+                   "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True,
+                                       check=True).stdout.split()))
+    S = _lib.Schedule
+    assert got == [ctypes.sizeof(S), S.deterministic.offset, S.workgroups.offset]
+
+
+def test_schedule_query_is_a_dry_run():
+    """The schedule query runs the launchers' decisions without launching: it works without a GPU
+    (no device: no split, no stream-K; the grids are the whole-tile ones) and reports the
+    workgroups each launch would take."""
+    L = _lib.lib()
+    d = _lib.Desc(8, 12, 12, 1024, 1024, 64, 1, 0, 0.0, _lib.DC_F32, 0, 0, 0, 0)
+    out = _lib.Schedule()
+    assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, 1 << 20, ctypes.byref(out)) == _lib.DC_OK
+    assert out.split_chunk == 0 and out.split_pieces == 1
+    assert out.workgroups == (1024 // 128) * 8 * 12  # 128-query tiles of every (b, h)
+    ws = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
+    assert L.dc_sdpa_bwd_schedule(ctypes.byref(d), 0, ws, ctypes.byref(out)) == _lib.DC_OK
+    assert out.streamk_ranges == 0
+    assert out.workgroups > (1024 // 128) * 8 * 12  # the pre-kernel, then one per key tile
+    # Errors are the call's own: a backward workspace below dsum is rejected.
+    assert L.dc_sdpa_bwd_schedule(ctypes.byref(d), 0, 0, ctypes.byref(out)) == _lib.DC_INVALID_ARGUMENT
+    bad = _lib.Desc(1, 3, 2, 4, 4, 8, 0, 0, 0.0, _lib.DC_F32, 0, 0, 0, 0)
+    assert L.dc_sdpa_fwd_schedule(ctypes.byref(bad), 0, 0, ctypes.byref(out)) == _lib.DC_INVALID_ARGUMENT
+    assert L.dc_last_error() == b"flash attention q/k/v shapes do not match"

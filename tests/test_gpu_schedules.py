@@ -46,11 +46,13 @@ def _forward_nan_filled(q, k, v, causal, dtype=None):
     d = _native._desc(dims, causal, None, dtype, (0, 0, 0))
     L_ = _lib.lib()
     ws = _native._workspace(L_.dc_sdpa_fwd_workspace_size(d), q.device)
+    sched = _native._schedule(False, q, k, v, causal, workspace_bytes=ws.numel())
+    print(f"[schedule] {sched}", flush=True)
     _lib.check(L_.dc_sdpa_fwd(d, _native._ptr(q), _native._ptr(k), _native._ptr(v), None,
                               _native._ptr(out), _native._ptr(lse), _native._ptr(ws), ws.numel(),
                               _native._stream(q.device)))
     torch.cuda.synchronize()
-    return out.float().cpu().numpy(), lse.cpu().numpy()
+    return out.float().cpu().numpy(), lse.cpu().numpy(), sched
 
 
 FWD_CASES = [  # tag, B, H, Hkv, L, S, E, causal
@@ -73,7 +75,8 @@ def test_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
     v = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
     print(f"[case] forward split {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
     ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
-    out, lse = _forward_nan_filled(q, k, v, causal)
+    out, lse, sched = _forward_nan_filled(q, k, v, causal)
+    assert sched["split_chunk"] > 0 and sched["split_pieces"] > 1, f"{tag}: no split ran: {sched}"
     assert_f32(out, ref_o, f"{tag} out")
     assert_f32(lse, ref_l, f"{tag} lse")
 
@@ -98,7 +101,8 @@ def test_bf16_forward_split_ranges(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
     v = bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32))
     print(f"[case] bf16 forward split {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
     ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
-    out, lse = _forward_nan_filled(q, k, v, causal, torch.bfloat16)
+    out, lse, sched = _forward_nan_filled(q, k, v, causal, torch.bfloat16)
+    assert sched["split_chunk"] > 0 and sched["f16_products"] == 1, f"{tag}: no split ran: {sched}"
     assert_bf16(out, ref_o, f"{tag} out")
     assert_bf16(lse, ref_l, f"{tag} lse")
 
@@ -135,6 +139,11 @@ def test_bf16_backward_split_grids(oracle_lib, tag, B, H, Hkv, L, S, E, causal):
     d = _native._desc(dims, causal, None, torch.bfloat16, (0, 0, 0))
     L_ = _lib.lib()
     ws = _native._workspace(L_.dc_sdpa_bwd_workspace_size(d), tq.device)
+    sched = _native._schedule(True, tq, tk, tv, causal, workspace_bytes=ws.numel())
+    print(f"[schedule] {sched}", flush=True)
+    assert sched["f16_products"] == 1 and (sched["split_chunk_k"] > 0 or sched["split_chunk_q"] > 0), \
+        f"{tag}: no split grid ran: {sched}"
+    assert sched["deterministic"] == 1
     _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(tg), _native._ptr(tq), _native._ptr(tk), _native._ptr(tv),
                               _native._ptr(out), _native._ptr(lse), None, _native._ptr(dq), _native._ptr(dk),
                               _native._ptr(dv), _native._ptr(ws), ws.numel(), _native._stream(tq.device)))
@@ -155,12 +164,14 @@ def _backward_nan_filled(g, q, k, v, out, lse, causal, mask=None):
     d = _native._desc(dims, causal, None, torch.float32, ms)
     L_ = _lib.lib()
     ws = _native._workspace(L_.dc_sdpa_bwd_workspace_size(d), q.device)
+    sched = _native._schedule(True, q, k, v, causal, mask=m, workspace_bytes=ws.numel())
+    print(f"[schedule] {sched}", flush=True)
     _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(g), _native._ptr(q), _native._ptr(k), _native._ptr(v),
                               _native._ptr(out), _native._ptr(lse), _native._ptr(m), _native._ptr(dq),
                               _native._ptr(dk), _native._ptr(dv), _native._ptr(ws), ws.numel(),
                               _native._stream(q.device)))
     torch.cuda.synchronize()
-    return [x.cpu().numpy() for x in (dq, dk, dv)]
+    return [x.cpu().numpy() for x in (dq, dk, dv)], sched
 
 
 CASES = [  # tag, B, H, Hkv, L, S, E, causal, mask
@@ -192,7 +203,11 @@ def test_backward_schedules(oracle_lib, tag, B, H, Hkv, L, S, E, causal, mask):
           flush=True)
     ref_o, ref_l = oracle_lib.forward(q, k, v, causal, None, m)
     rq, rk, rv = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal, None, m)
-    dq, dk, dv = _backward_nan_filled(g, q, k, v, ref_o, ref_l, causal, m)
+    (dq, dk, dv), sched = _backward_nan_filled(g, q, k, v, ref_o, ref_l, causal, m)
+    if tag.startswith("whole"):
+        assert sched["streamk_ranges"] == 0, f"{tag}: expected whole key tiles: {sched}"
+    else:
+        assert sched["streamk_ranges"] > 0, f"{tag}: expected the stream-K schedule: {sched}"
     assert_f32(dq, rq, f"{tag} dq")
     assert_f32(dk, rk, f"{tag} dk")
     assert_f32(dv, rv, f"{tag} dv")
@@ -219,6 +234,8 @@ def test_split_shapes_without_split_workspace(oracle_lib, dtype):
     stream = _native._stream(tq.device)
     print(f"[case] reduced workspaces {dtype} B{B} H{H} L{L} E{E}", flush=True)
     assert L_.dc_sdpa_fwd_workspace_size(d) > 256  # the full size holds split partials
+    assert _native._schedule(False, tq, tk, tv, causal)["split_chunk"] > 0
+    assert _native._schedule(False, tq, tk, tv, causal, workspace_bytes=0)["split_chunk"] == 0
     out = torch.full((B, H, L, E), float("nan"), device=DEV, dtype=dt)
     lse = torch.full((B, H, L), float("nan"), device=DEV)
     _lib.check(L_.dc_sdpa_fwd(d, _native._ptr(tq), _native._ptr(tk), _native._ptr(tv), None, _native._ptr(out),
@@ -233,6 +250,13 @@ def test_split_shapes_without_split_workspace(oracle_lib, dtype):
     dsum_bytes = (B * H * L * 4 + 255) // 256 * 256
     less = full - 1 if bf16 else dsum_bytes
     ws = _native._workspace(less, tq.device)
+    full_sched = _native._schedule(True, tq, tk, tv, causal)
+    less_sched = _native._schedule(True, tq, tk, tv, causal, workspace_bytes=less)
+    print(f"[schedule] full {full_sched} reduced {less_sched}", flush=True)
+    if bf16:
+        assert full_sched["split_chunk_k"] > 0 or full_sched["split_chunk_q"] > 0
+        assert less_sched["split_chunk_k"] == 0 and less_sched["split_chunk_q"] == 0
+        assert less_sched["f16_products"] == 1
     dq, dk, dv = (torch.full((B, H, L, E), float("nan"), device=DEV, dtype=dt) for _ in range(3))
     o_in = out if bf16 else _t(ref_o)
     l_in = lse if bf16 else torch.from_numpy(ref_l).to(DEV)
