@@ -17,7 +17,7 @@ EXPORTS = ("dc_abi_version", "dc_last_error",
            "dc_sdpa_fwd_workspace_size", "dc_sdpa_fwd",
            "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
            "dc_sdpa_decode_workspace_size", "dc_sdpa_decode",
-           "dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule",
+           "dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule", "dc_sdpa_decode_noalloc",
            "dc_softmax_fwd", "dc_softmax_bwd",
            "dc_mt19937_seed", "dc_mt19937_advance", "dc_mt19937_table_bytes",
            "dc_mt19937_table_init", "dc_bernoulli_max_draws", "dc_bernoulli_workspace_size",
@@ -75,6 +75,8 @@ def lib():
         L.dc_sdpa_fwd.argtypes = [D, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_bwd.argtypes = [D, P, P, P, P, P, P, P, P, P, P, P, SZ, P]
         L.dc_sdpa_decode.argtypes = [D, P, P, P, P, P, P, SZ, P]
+        L.dc_sdpa_decode_noalloc.argtypes = [D, P, P, P, P, P, P]
+        L.dc_sdpa_decode_noalloc.restype = ctypes.c_int
         for name in ("dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule"):
             getattr(L, name).argtypes = [D, ctypes.c_int, SZ, ctypes.POINTER(Schedule)]
             getattr(L, name).restype = ctypes.c_int

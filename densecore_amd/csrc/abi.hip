@@ -435,6 +435,37 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
     return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
 }
 
+dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                                 void *out, float *lse, void *stream) {
+    dc::AttnShape s;
+    dc_status st = check_dims(d, &s);
+    if (st != DC_OK) return st;
+    if (s.L != 1) return fail(DC_INVALID_ARGUMENT, "flash attention decode takes q_len == 1");
+    if (s.causal)
+        return fail(DC_INVALID_ARGUMENT,
+                    "flash attention decode is non-causal (top-left causal at L = 1 sees one key)");
+    const size_t need = decode_ws(s);
+    if (need > dc::kDecodeScratchBytes)
+        return fail(DC_UNSUPPORTED, "flash attention decode needs " + std::to_string(need) +
+                                        " bytes of split partials, more than the " +
+                                        std::to_string(dc::kDecodeScratchBytes) +
+                                        " bytes of scratch the allocation-free entry point holds "
+                                        "(batch * heads too large); use dc_sdpa_decode with a workspace");
+    const int64_t nq = (int64_t)s.B * s.H, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
+    if (nq == 0) return ok();
+    if (!present(q, nq * s.E) || !present(k, nkv) || !present(v, nkv) ||
+        !present(out, nq * s.E) || !present(lse, nq))
+        return fail(DC_INVALID_ARGUMENT, kNullMsg);
+    s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    dc::DecodeArgs a{};
+    a.s = s;
+    a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
+    st = launched(dc::decode_scratch(&a.part));  // the device address, never the array's name
+    if (st != DC_OK) return st;
+    a.splits = dc::decode_splits(s, &a.split_len);
+    return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
+}
+
 dc_status dc_softmax_fwd(const dc_softmax_desc *d, const float *x, const float *mask, float *y,
                          void *stream) {
     dc::SoftmaxArgs a;

@@ -14,11 +14,24 @@
 //     p * v per lane, reduced across row groups and waves through LDS;
 //   * each split writes (acc[E], max, sum) to the workspace; a merge kernel rescales and sums
 //     the splits per head and writes out and lse.
+#include <mutex>
+
 #include "common.hpp"
 #include "params.hpp"
 
 namespace dc {
 namespace {
+
+// Scratch of the allocation-free entry point (dc_sdpa_decode_noalloc): the split partials live
+// in this file-scope array instead of a caller's workspace.  Each GPU the library runs on holds
+// its own copy, at its own address, until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in): it passes the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch[kMaxDevices];
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -228,6 +241,20 @@ int decode_splits(const AttnShape &s, int *split_len) {
 
 hipError_t launch_decode(const DecodeArgs &a, bool bf16, hipStream_t st) {
     return bf16 ? launch_dtype<__bf16>(a, st) : launch_dtype<float>(a, st);
+}
+
+hipError_t decode_scratch(float **ptr) {
+    int dev = -1;
+    return_if(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        return_if(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[dev] = static_cast<float *>(p);
+    }
+    *ptr = g_scratch[dev];
+    return hipSuccess;
 }
 
 }  // namespace dc

@@ -115,6 +115,10 @@ hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);
 size_t bwd_bf16_split_bytes(const AttnShape &s);
 hipError_t launch_decode(const DecodeArgs &a, bool bf16, hipStream_t st);
 int decode_splits(const AttnShape &s, int *split_len);
+// The allocation-free decode's scratch (a static device array in decode.hip): its size, and its
+// address on the current device (looked up with hipGetSymbolAddress once per device).
+constexpr size_t kDecodeScratchBytes = (size_t)16 << 20;
+hipError_t decode_scratch(float **ptr);
 // `vec`: rows (and mask rows) start 16-byte aligned and the width is a multiple of 4.
 hipError_t launch_softmax_fwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
 hipError_t launch_softmax_bwd(const SoftmaxArgs &a, bool vec, hipStream_t st);

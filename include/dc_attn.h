@@ -98,6 +98,17 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
                          void *out, float *lse, void *workspace, size_t workspace_bytes,
                          void *stream);
 
+/* dc_sdpa_decode without a workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  It allocates nothing: the split partials go to a static device array of
+ * 16 MiB (16 << 20 bytes) that each GPU the library runs on holds until the process ends, so
+ * batch * heads * splits * (head_dim + 2) * 4 bytes (dc_sdpa_decode_workspace_size) must fit in
+ * it, else DC_UNSUPPORTED.  Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other threads) race and must not be issued.  Results are identical to
+ * dc_sdpa_decode's. */
+dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const void *k, const void *v,
+                                 void *out, float *lse, void *stream);
+
 /* Message of the last non-DC_OK status on the calling thread ("" if none). */
 const char *dc_last_error(void);
 
