@@ -71,6 +71,48 @@ def roofline(achieved, peak, unit, bound, traffic, kernel, work_note):
             "work": work_note}
 
 
+def parity(got, ref, bf16=False):
+    """Margins of one output against the oracle: max |gpu - ref|, the normwise relative error,
+    and the largest fraction of the elementwise bar used (<= 1 passes): float32
+    |gpu - ref| <= 2e-5 + 1e-5 |ref|; bf16 |gpu - ref| <= 1e-2 |ref| + 1e-2 rms(ref)."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    diff = np.abs(got - ref)
+    if bf16:
+        bar = 1e-2 * np.abs(ref) + 1e-2 * float(np.sqrt(np.mean(ref ** 2)))
+    else:
+        bar = 2e-5 + 1e-5 * np.abs(ref)
+    used = diff / np.maximum(bar, 1e-300)
+    nref = float(np.linalg.norm(ref))
+    return {"max_abs": float(np.nanmax(diff)) if diff.size else 0.0,
+            "normwise_rel": float(np.linalg.norm(diff) / nref) if nref else 0.0,
+            "bar_used": float(np.nanmax(used)) if used.size else 0.0,
+            "allclose": bool(np.all(diff <= bar))}
+
+
+def host_cpus():
+    """This host's CPUs as the CPU baseline sees them: `nproc` (the affinity mask), the cgroup
+    CPU quota when one is set, and the CPU model."""
+    nproc = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+            if q != "max":
+                quota = float(q) / float(per)
+    except (OSError, ValueError):
+        pass
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return nproc, quota, model
+
+
 def bench_prefill(torch, native, name, steps, warmup, dev):
     """Forward (+ backward) of a prefill config; returns per-call mean ms and throughput."""
     from tests._data import CONFIGS, make_inputs, additive
@@ -110,7 +152,20 @@ def bench_prefill(torch, native, name, steps, warmup, dev):
         out, lse = fwd()
         res["bwd_ms"] = kernel_ms(torch, stream, lambda: native._flash_attention_backward(
             g, q, k, v, out, lse, causal, scale, mask), n)
+    # One more call whose outputs the CPU-baseline leg checks against the oracle (C5: the
+    # (b = 0, h < 16) slice the CPU leg computes).
+    sl = (slice(0, 1), slice(0, 16)) if name == "C5" else (slice(None), slice(None))
+    out, lse = fwd()
+    keep = {"out": out[sl].float().cpu().numpy(), "lse": lse[sl].cpu().numpy()}
+    if bwd:
+        grads = native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask)
+        keep.update({n: t[sl].float().cpu().numpy() for n, t in zip(("dq", "dk", "dv"), grads)})
+        del grads
+    torch.cuda.synchronize()
+    res["outputs"] = keep
     ff, fb = flops(B, H, L, S, E, causal, bwd)
+    if name == "C2":
+        res["public"] = bench_public(torch, q, k, v, g, steps, warmup, ff + fb)
     if name == "C3":  # useful work counts valid keys only
         ff = 4.0 * H * L * E * float(np.sum(d["lengths"]))
     res.update({"fwd_flop": ff, "bwd_flop": fb})
@@ -119,6 +174,29 @@ def bench_prefill(torch, native, name, steps, warmup, dev):
     if bwd:
         res["bwd_tflops"] = fb / (res["bwd_ms"] * 1e-3) / 1e12
     return res
+
+
+def bench_public(torch, q, k, v, g, steps, warmup, work):
+    """C2 through the public API: ``functional.scaled_dot_product_attention`` on leaf tensors
+    that require gradients, then the gradients by autograd (the flash autograd node saves out
+    and lse and calls the backward), wall clock over the steps."""
+    from densecore_amd import functional as F
+    qr, kr, vr = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        out = F.scaled_dot_product_attention(qr, kr, vr, is_causal=True)
+        torch.autograd.grad(out, (qr, kr, vr), g)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    return {"ms_per_step": round(ms, 4), "tflops": round(work / (ms * 1e-3) / 1e12, 3),
+            "path": "functional.scaled_dot_product_attention + torch.autograd.grad (flash node)"}
 
 
 def bench_decode(torch, native, steps, warmup, dev):
@@ -139,8 +217,10 @@ def bench_decode(torch, native, steps, warmup, dev):
     n = max(steps, 10)
     ev = kernel_ms(torch, stream, lambda: native._flash_decode(q, k, v), n)
     nbytes = decode_bytes(B, H, S, E)
+    out, lse = native._flash_decode(q, k, v)
+    keep = {"out": out.cpu().numpy(), "lse": lse.cpu().numpy()}
     return {"ms_per_step": wall, "event_ms": ev, "bytes": nbytes, "timing_calls": n,
-            "gbps": nbytes / (ev * 1e-3) / 1e9}
+            "gbps": nbytes / (ev * 1e-3) / 1e9, "outputs": keep}
 
 
 def bench_math(torch, steps, warmup, dev):
@@ -204,44 +284,83 @@ def bench_math(torch, steps, warmup, dev):
     return res
 
 
-def cpu_baseline(threads):
-    """The oracle (C port of DenseCore's CPU SDPA) on this host's cores: the full C2 workload
-    (the headline figure, median of 2) and, once each, full C1, C3 (the reference's materialised
-    (B, H, L, S) mask) and C4, in the units of their GPU figures, plus the math path's softmax
-    and Bernoulli draws on a slice of C3's shape."""
+def cpu_baseline(threads, gpu):
+    """The oracle (C port of DenseCore's CPU SDPA) on this host's cores, in the units of the GPU
+    figures: the full C2 workload (the headline figure, median of 2), full C1, C3 (the
+    reference's materialised (B, H, L, S) mask) and C4 once each, and a slice of C5 (b = 0,
+    h < 16: 16 of its 64 whole (batch, head) tasks, forward and backward) extrapolated to the
+    whole config; plus the math path's softmax and Bernoulli draws on a slice of C3's shape.
+
+    The oracle's outputs of these runs are also the checker of the GPU's outputs of the same
+    inputs (``gpu``: name -> host copies): ``parity`` gives each output's margins against the
+    bar.  C5's backward takes the GPU's own bf16 out and lse, as the GPU backward did."""
     import oracle
     from tests._data import additive, make_inputs
     oracle.build()
     oracle.set_num_threads(threads)
+    checks = {}
+
+    def check(name, got, ref, bf16=False):
+        if got is not None:
+            checks[name] = {k: parity(got[k], r, bf16) for k, r in ref.items()}
+
     d = make_inputs("C2")
     times = []
     for _ in range(2):
         t0 = time.perf_counter()
         o, l = oracle.forward(d["q"], d["k"], d["v"], True)
-        oracle.backward(d["g"], d["q"], d["k"], d["v"], o, l, True)
+        grads = oracle.backward(d["g"], d["q"], d["k"], d["v"], o, l, True)
         times.append(time.perf_counter() - t0)
+    check("C2", gpu.get("C2"), dict(zip(("out", "lse", "dq", "dk", "dv"), (o, l) + tuple(grads))))
     ff, fb = flops(8, 12, 1024, 1024, 64, True, True)
     best = float(np.median(times))
     per = {}
     d = make_inputs("C1")
     t0 = time.perf_counter()
-    oracle.forward(d["q"], d["k"], d["v"], True)
+    o, l = oracle.forward(d["q"], d["k"], d["v"], True)
     dt = time.perf_counter() - t0
+    check("C1", gpu.get("C1"), {"out": o, "lse": l})
     per["C1"] = {"tflops": round(flops(64, 6, 256, 256, 64, True, False)[0] / dt / 1e12, 5),
                  "s": round(dt, 3)}
     d = make_inputs("C3")
     mask = additive(d["mask_bool"], (16, 16, 512, 512))
     t0 = time.perf_counter()
-    oracle.forward(d["q"], d["k"], d["v"], False, None, mask)
+    o, l = oracle.forward(d["q"], d["k"], d["v"], False, None, mask)
     dt = time.perf_counter() - t0
+    check("C3", gpu.get("C3"), {"out": o, "lse": l})
     per["C3"] = {"tflops": round(4.0 * 16 * 512 * 64 * float(np.sum(d["lengths"])) / dt / 1e12, 5),
                  "s": round(dt, 3), "note": "useful FLOPs (valid keys); the CPU path computes every key"}
     del mask
     d = make_inputs("C4")
     t0 = time.perf_counter()
-    oracle.forward(d["q"], d["k"], d["v"], False)
+    o, l = oracle.forward(d["q"], d["k"], d["v"], False)
     dt = time.perf_counter() - t0
+    check("C4", gpu.get("C4"), {"out": o, "lse": l})
     per["C4"] = {"gbps": round(decode_bytes(32, 32, 4096, 128) / dt / 1e9, 2), "s": round(dt, 3)}
+    del d, o, l
+    # C5: 16 whole (batch, head) tasks (each independent, bit-identical under any thread split,
+    # src/torch_attention.rs:8) on the exact float32 upcast of the bf16 inputs.
+    c5 = gpu.get("C5")
+    if c5 is not None:
+        d = make_inputs("C5")
+        sl = (slice(0, 1), slice(0, 16))
+        q, k, v, g = (np.ascontiguousarray(d[n][sl]) for n in ("q", "k", "v", "g"))
+        del d
+        t0 = time.perf_counter()
+        o, l = oracle.forward(q, k, v, True)
+        tf = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        grads = oracle.backward(g, q, k, v, c5["out"], c5["lse"], True)
+        tb = time.perf_counter() - t0
+        check("C5", c5, dict(zip(("out", "lse", "dq", "dk", "dv"), (o, l) + tuple(grads))), bf16=True)
+        fwd5, bwd5 = flops(2, 32, 8192, 8192, 128, True, True)
+        scale = 64 / 16
+        per["C5"] = {"tflops": round((fwd5 + bwd5) / ((tf + tb) * scale) / 1e12, 5),
+                     "s_slice": round(tf + tb, 3), "s_full_extrapolated": round((tf + tb) * scale, 3),
+                     "extrapolated": True,
+                     "sample": "b = 0, h < 16: 16 of C5's 64 (batch, head) tasks, forward + backward, "
+                               "x4 for the whole config"}
+        del q, k, v, g, o, l, grads
     # The math path's pieces at C3's shape, single-threaded as the reference runs them:
     # softmax_lastdim over 8 of the 256 (b, h) score blocks and Generator::bernoulli draws.
     x = np.random.default_rng(0).standard_normal((8, 512, 512), dtype=np.float32)
@@ -257,11 +376,13 @@ def cpu_baseline(threads):
                         "bernoulli_gdraws_per_s": round(n / db / 1e9, 4), "threads": 1,
                         "sample": f"softmax of {x.size} scores (8 of C3's 256 blocks, {dt:.3f} s), "
                                   f"{n} Bernoulli draws (an eighth of C3's, {db:.3f} s)"}
-    return {"value": round((ff + fb) / best / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
+    nproc, quota, model = host_cpus()
+    base = {"value": round((ff + fb) / best / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "nproc": nproc, "cgroup_cpus": quota, "cpu_model": model,
             "sample": f"full C2 fwd+bwd (B8 H12 T1024 D64 fp32) x{len(times)}, median "
                       f"{best:.2f} s; oracle/sdpa_oracle.c, {threads} threads",
             "configs": per}
+    return base, checks
 
 
 # Shapes whose whole-tile grids fill little of the device (few heads, long rows), where the
@@ -369,6 +490,7 @@ def main():
             f"{c2['fwd_flop'] / 1e9:.3f} GFLOP per call / {c2['fwd_ms']:.4f} ms (HIP events around "
             f"{c2['timing_calls']} back-to-back calls)")
         line["mfma_frac"] = round(c2["tflops"] / PEAK_FP32_MFMA, 4)
+        line["public_api"] = c2["public"]
     c4 = results.get("C4")
     if c4:
         line["decode"] = {"workload": "C4: decode fp32, B=32 H=32 S=4096 D=128, split-KV",
@@ -400,8 +522,15 @@ def main():
     if results.get("sched"):
         line["schedules"] = results["sched"]
     if not args.no_cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        line["cpu_baseline"] = cpu_baseline(threads)
+        # The reference's default is every core it may run on (std::thread::available_parallelism,
+        # src/torch_sum.rs:48): `nproc`, bounded by the cgroup's CPU quota and by the GPU box's CPU
+        # share (16 per GPU).
+        nproc, quota, _ = host_cpus()
+        threads = max(1, min(nproc, int(quota) if quota else nproc, 16))
+        gpu = {name: r["outputs"] for name, r in results.items() if isinstance(r, dict) and "outputs" in r}
+        line["cpu_baseline"], line["parity"] = cpu_baseline(threads, gpu)
+        line["parity_note"] = ("GPU outputs of the bench configs against the oracle's outputs of the "
+                               "same inputs from the cpu_baseline leg; bar_used <= 1 passes")
     print(json.dumps(line), flush=True)
 
 

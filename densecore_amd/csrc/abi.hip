@@ -147,11 +147,13 @@ size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
     return n;
 }
 
-// The backward's workspace: dsum (B*H*L floats; float32 accumulates dQ in its output), then for
-// bf16 the scaled fp16 copies of q, k, v, dout with their per-slab scratch, then the float32
-// partials of split grids (small grids on the current device; none otherwise).
+// The backward's workspace: dsum (B*H*L floats), then for float32 the deterministic partials
+// (each key tile's dQ slot and the stream-K cut tiles' dK / dV slots; without them dQ is
+// accumulated in its output with atomics), for bf16 the scaled fp16 copies of q, k, v, dout with
+// their per-slab scratch, then the float32 partials of split grids (small grids on the current
+// device; none otherwise).
 struct BwdLayout {
-    size_t dsum, q16, k16, v16, do16, partial, exps, copies_end, split, total;
+    size_t dsum, part, q16, k16, v16, do16, partial, exps, copies_end, split, total;
 };
 BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     BwdLayout l{};
@@ -162,6 +164,8 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
         return off;
     };
     l.dsum = take((size_t)s.B * s.H * s.L * sizeof(float));
+    l.part = at;
+    if (!bf16) take(dc::bwd_f32_part_bytes(s));
     if (bf16) {
         const size_t nq = (size_t)s.B * s.H * s.L * s.E, nk = (size_t)s.B * s.Hkv * s.S * s.E;
         const int64_t qslab = (int64_t)s.repeat * s.L * s.E, kslab = (int64_t)s.S * s.E;
@@ -180,8 +184,9 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     return l;
 }
 size_t bwd_ws(const dc::AttnShape &s, bool bf16) { return bwd_layout(s, bf16).total; }
-// The least the backward needs (dsum): the bf16 fp16 copies are used only when they fit.
-size_t bwd_ws_min(const dc::AttnShape &s) { return bwd_layout(s, false).total; }
+// The least the backward needs (dsum): the float32 deterministic partials and the bf16 fp16
+// copies are used only when they fit.
+size_t bwd_ws_min(const dc::AttnShape &s) { return bwd_layout(s, false).part; }
 
 size_t decode_ws(const dc::AttnShape &s) {
     int split_len = 0;
@@ -339,8 +344,12 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     a.dq = dq, a.dk = dk, a.dv = dv;
     a.dsum = reinterpret_cast<float *>(ws);
     a.dq_acc = bf16 ? nullptr : static_cast<float *>(dq);
-    // bf16: the fp16 products when the workspace holds the copies (else the bf16 hi + lo pairs).
     const BwdLayout l = bwd_layout(s, bf16);
+    if (!bf16 && workspace_bytes > l.part) {
+        a.dq_part = reinterpret_cast<float *>(ws + l.part);
+        a.part_bytes = workspace_bytes - l.part;
+    }
+    // bf16: the fp16 products when the workspace holds the copies (else the bf16 hi + lo pairs).
     if (bf16 && workspace_bytes >= l.copies_end) {
         a.q16 = ws + l.q16, a.k16 = ws + l.k16, a.v16 = ws + l.v16, a.do16 = ws + l.do16;
         a.f16_partial = reinterpret_cast<float *>(ws + l.partial);

@@ -5,9 +5,14 @@
 //   dsum = rowsum(dO * O);  P = exp(scale * q k^T + mask - lse) (0 where causal-masked);
 //   dV = P^T dO;  dP = dO V^T;  dS = P * (dP - dsum);  dQ = scale dS K;  dK = scale dS^T Q,
 // accumulating over the query heads that share a kv head (:321-324).  Everything accumulates
-// in float32; P and dS enter their products as two bf16 terms each (hi = bf16(x),
-// lo = bf16(x - hi)), so they are carried to about 2^-17, and the only bf16 roundings left
-// are those of the outputs.
+// in float32.  The products run in one of two forms:
+//   * with the workspace's fp16 copies (the default): q, k, v and dO are copied to fp16, each
+//     (batch, kv head) slab scaled by a power of two (exact for its bf16 values, f16_stage.hip);
+//     P and dS are rounded once to fp16 (2^-12), and an MFMA block in which some P exceeds kLoP
+//     also takes the rounding error of its P and dS as a second fp16 term (about 2^-22);
+//   * without them (a workspace of dsum alone): the bf16 inputs themselves, with P and dS as two
+//     bf16 terms each (hi = bf16(x), lo = bf16(x - hi)), carried to about 2^-17.
+// Either way the only bf16 roundings of the results are those of the outputs.
 //
 // Two kernels, neither with atomics (dQ is deterministic):
 //   * bwd_dkdv_bf16_kernel (keys stationary): a workgroup of 8 waves owns 128 keys of one
@@ -94,6 +99,20 @@ DEVI F16Scales f16_scales(const BwdArgs &a, int bhk) {
     return f;
 }
 
+// The fp16 products round P and dS once, to 2^-12 of each term.  Where large terms cancel
+// (early keys of a long causal row get P ~ 1 / (query + 1) from the nearby queries while their
+// dV sums thousands of terms to something small) that rounding alone reaches 1% of rms(dV) at
+// L = 8192.  So an MFMA block (16 queries x 32 keys, or 16 keys x 32 queries) in which some P
+// exceeds kLoP also multiplies the rounding error of its P and dS (cvt_f16x8_lo) in a second
+// product: those terms are then carried to about 2^-22.  On N(0, 1) inputs at C5's shape about
+// 1% of the blocks take it (the early queries); the largest dV error falls from 0.97 of the bf16
+// bar to 0.16 (float64 simulation of head 7 of C5).
+constexpr float kLoP = 0x1p-4f;
+// The dK/dV kernel forms P times 2^kPShift (folded into the exponent) so that the low parts of
+// P >= kLoP are normal fp16 numbers (>= 2^-2); dV is scaled back at the end (P <= 1, so P times
+// 2^14 stays below fp16's largest value even for an lse a few units off).
+constexpr int kPShift = 14;
+
 template <bool F16>
 DEVI f32x16 mfma16(bf16x8 x, bf16x8 y, f32x16 c) {
     if constexpr (F16) return mfma_f16(x, y, c);
@@ -174,7 +193,8 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     // rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
     auto load_row_stat = [&](int i) -> float {
         const int bh = step_bh(i), qq = step_m0(i) + lane;
-        if (wave == 0) return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e : -INFINITY;
+        if (wave == 0)
+            return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e + (F16 ? (float)kPShift : 0.f) : -INFINITY;
         const float ds = qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
         return F16 ? ldexpf(ds, fs.e_pv) : ds;
     };
@@ -247,7 +267,7 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                         if (EDGE && (key >= s.S || (CAUSAL && key > qq))) x = -INFINITY;
                         const float p = exp2_fast(x);
                         sacc[r] = p;
-                        pacc[r] = F16 ? p * (pacc[r] - dsm[j]) * 0x1p-24f : p * (pacc[r] - dsm[j]);
+                        pacc[r] = F16 ? p * (pacc[r] - dsm[j]) * 0x1p-38f : p * (pacc[r] - dsm[j]);
                     }
                 }
             };
@@ -259,16 +279,22 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
             for (int u = 0; u < 2; ++u) {
                 const int row0 = 32 * qh + 16 * u;
                 bf16x8 ph, pl;
-                if constexpr (F16) ph = cvt_f16x8(sacc, 8 * u);
-                else split_bf16(sacc, 8 * u, ph, pl);
+                bool lo = false;  // F16: this block's P and dS also enter as their rounding errors
+                if constexpr (F16) {
+                    ph = cvt_f16x8(sacc, 8 * u);
+                    lo = any_above(sacc, 8 * u, kLoP * (float)(1 << kPShift));
+                } else {
+                    split_bf16(sacc, 8 * u, ph, pl);
+                }
                 bf16x8 fa[NDT];
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(ot, trb, row0, dt);
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma16<F16>(fa[dt], ph, dv[dt]);
-                if constexpr (!F16) {
+                if (!F16 || lo) {
+                    if constexpr (F16) pl = cvt_f16x8_lo(sacc, 8 * u, ph);
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma_bf16(fa[dt], pl, dv[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma16<F16>(fa[dt], pl, dv[dt]);
                 }
                 if constexpr (F16) ph = cvt_f16x8(pacc, 8 * u);
                 else split_bf16(pacc, 8 * u, ph, pl);
@@ -276,9 +302,10 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(qt, trb, row0, dt);
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma16<F16>(fa[dt], ph, dk[dt]);
-                if constexpr (!F16) {
+                if (!F16 || lo) {
+                    if constexpr (F16) pl = cvt_f16x8_lo(pacc, 8 * u, ph);
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma_bf16(fa[dt], pl, dk[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma16<F16>(fa[dt], pl, dk[dt]);
                 }
             }
         }
@@ -309,7 +336,7 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
             dv[dt][r] += sm.r.acc[kw][NDT + dt][r][lane];
             if constexpr (F16) {  // undo the copies' scales (exact powers of two)
                 dk[dt][r] = ldexpf(dk[dt][r], -(fs.e_q + fs.e_pv - 24));
-                dv[dt][r] = ldexpf(dv[dt][r], -fs.e_do);
+                dv[dt][r] = ldexpf(dv[dt][r], -(fs.e_do + kPShift));
             }
         }
     if (SPLIT && npieces > 1) {
@@ -494,7 +521,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             // Keep the operand reads (one per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 1, 4>();
             // dS^T; EDGE (keys past S or past the diagonal) is a separate instantiation so
-            // that the common path carries no per-element masking.
+            // that the common path carries no per-element masking.  big[u]: some P of the
+            // 16-key half u exceeds kLoP (its dS then also enters as its rounding error).
+            bool big[2] = {false, false};
             auto elementwise = [&](auto edge_c) {
                 constexpr bool EDGE = decltype(edge_c)::value;
 #pragma unroll
@@ -507,6 +536,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                         const int key = n0 + kt * 32 + acc_row(r, g);
                         if (key >= s.S || (CAUSAL && key > qi)) x = -INFINITY;
                     }
+                    if (F16) big[r >> 3] |= x > -4.f;  // P = 2^x > kLoP = 2^-4
                     sacc[r] = F16 ? exp2_fast(x) * (pacc[r] - dsum_q) * 0x1p-24f
                                   : exp2_fast(x) * (pacc[r] - dsum_q);
                 }
@@ -517,16 +547,22 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 bf16x8 sh, sl;
-                if constexpr (F16) sh = cvt_f16x8(sacc, 8 * u);
-                else split_bf16(sacc, 8 * u, sh, sl);
+                bool lo = false;  // F16: this block's dS also enters as its rounding error
+                if constexpr (F16) {
+                    sh = cvt_f16x8(sacc, 8 * u);
+                    lo = __builtin_amdgcn_ballot_w64(big[u]) != 0;
+                } else {
+                    split_bf16(sacc, 8 * u, sh, sl);
+                }
                 bf16x8 fa[NDT];
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kQN, D>(kt_, trb, 32 * kt + 16 * u, dt);
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[dt], sh, dq[dt]);
-                if constexpr (!F16) {
+                if (!F16 || lo) {
+                    if constexpr (F16) sl = cvt_f16x8_lo(sacc, 8 * u, sh);
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma_bf16(fa[dt], sl, dq[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[dt], sl, dq[dt]);
                 }
             }
         }

@@ -14,15 +14,24 @@
 //   * the next step's Q, dO, lse and dsum are loaded into registers while a step computes;
 //   * dQ needs dS with queries on lanes: the four waves write their dS into one shared 32 x 128
 //     LDS tile, and after the next barrier each wave multiplies its share of it by the K tile
-//     (kept in LDS) into disjoint 16 x 16 blocks of dQ, which go to the float32 dQ
-//     accumulator with one coalesced global atomic per element and workgroup step.  That
-//     product runs between the next step's two barriers, so it costs no barrier of its own.
-// A small pre-kernel computes dsum and clears the dQ accumulator.
+//     (kept in LDS) into disjoint 16 x 16 blocks of the step's 32 x D dQ share.  That product
+//     runs between the next step's two barriers, so it costs no barrier of its own.
+// A small pre-kernel computes dsum.
+//
+// dQ is the sum of the key tiles' shares.  With the full workspace each tile stores its shares
+// in a slot of its own (the query rows its steps cover) and a reduction kernel adds the slots
+// in tile order, so dq is identical from run to run (the reference's guarantee,
+// src/torch_attention.rs:8); with the minimum workspace (dsum only) the shares are added into
+// dq with float atomics (the pre-kernel clears it first).
 //
 // When whole key tiles would leave part of the device idle (fewer tiles than workgroups that fit
 // at once, or a ragged last wave of equal non-causal tiles), a stream-K schedule replaces the
 // one-workgroup-per-tile grid: as many workgroups as fit at once each take an equal range of
-// the steps of all tiles, and tiles cut between ranges add their dK / dV atomically.
+// the steps of all tiles.  A tile cut between ranges gets its dK / dV as the sum of the ranges'
+// shares: stored in per-range slots and added in range order by the reduction (or, with the
+// minimum workspace, added atomically).
+#include <algorithm>
+
 #include "bwd_common.hpp"
 #include "common.hpp"
 #include "params.hpp"
@@ -104,16 +113,19 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
     }
 }
 
-// dQ[m0 .. m0+31][:] += scale * dS K for the step whose dS is in sm.ds.  The 32 x D tile is
-// split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32: lane l supplies
-// A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element gets exactly
-// one global atomic per workgroup step.  The reduction index is permuted so that a lane's four
+// The dQ share of the step whose dS is in sm.ds: scale * dS K for its 32 queries, rows
+// m0 .. m0 + 31.  `dst` points at row m0 of the destination (row stride E); rows at or past
+// `nrows` are not written.  ATOMIC adds scale * dS K into the float32 dq with float atomics;
+// otherwise dS K is stored (the reduction applies the scale) into the tile's own dQ slot.  The
+// 32 x D tile is split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32: lane l supplies
+// A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element is written
+// exactly once per workgroup step.  The reduction index is permuted so that a lane's four
 // steps over a 16-key block take four consecutive keys: step u of block kb gives lane l key
 // 16 kb + 4 (l/16) + u, and its dS and K^T operands for the block are one ds_read_b128 each.
 // Keys are covered in whole blocks up to nkeys rounded up to 16; the extra keys lie in the
 // same 32-key wave group as key nkeys - 1, whose dS columns this step wrote (zeros past S).
 template <int D>
-DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L, int E,
+DEVI void dq_product(const BwdSmem<D> &sm, float *dst, bool atomic, int nrows, int nkeys, int E,
                      float scale, int wave, int lane) {
     constexpr int TPW = D / 32;
     constexpr int NB = kBN / 16;  // 16-key blocks in a full tile
@@ -156,8 +168,11 @@ DEVI void dq_product(const BwdSmem<D> &sm, float *dqb, int m0, int nkeys, int L,
         const int d = dbase + 16 * j + r16;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int qq = m0 + qh * 16 + 4 * c4 + v;
-            if (qq < L && d < E) unsafeAtomicAdd(dqb + (int64_t)qq * E + d, acc[j][v] * scale);
+            const int r = qh * 16 + 4 * c4 + v;
+            if (r < nrows && d < E) {
+                if (atomic) unsafeAtomicAdd(dst + (int64_t)r * E + d, acc[j][v] * scale);
+                else dst[(int64_t)r * E + d] = acc[j][v];
+            }
         }
     }
 }
@@ -171,6 +186,18 @@ __host__ __device__ inline int tile_per_head(const AttnShape &s, int kt) {
     return s.L > m_begin ? (s.L - m_begin + kBM - 1) / kBM : 0;
 }
 __host__ __device__ inline int tile_steps(const AttnShape &s, int kt) { return tile_per_head(s, kt) * s.repeat; }
+
+// The dQ slots of the deterministic backward: key tile kt's slot holds, for every (batch, head),
+// the query rows its steps cover, [slot_from(kt), L) (causal: from the tile's first key; else all
+// rows).  slot_before(kt): rows of the slots of tiles 0 .. kt - 1, per (batch, head).
+__host__ __device__ inline int slot_from(const AttnShape &s, int kt) {
+    return s.causal ? (int)min((int64_t)kt * kBN, (int64_t)s.L) : 0;
+}
+__host__ __device__ inline int64_t slot_before(const AttnShape &s, int kt) {
+    if (!s.causal) return (int64_t)kt * s.L;
+    const int64_t j = min((int64_t)kt, ((int64_t)s.L + kBN - 1) / kBN);  // tiles starting before L
+    return j * s.L - (int64_t)kBN * j * (j - 1) / 2;
+}
 
 // Stream-K schedule: the steps of all key tiles, in (batch * kv head, key tile, step) order, cut
 // into `chunks` equal ranges, one per workgroup.  A key tile whose steps fall in more than one
@@ -186,10 +213,13 @@ __host__ __device__ inline int64_t chunk_of(const StreamK &k, int64_t p) {
     return ((p + 1) * k.chunks - 1) / k.total;
 }
 
-// Steps [i0, i1) of key tile kt of (batch, kv head) bhk, by one workgroup; `whole`: these are all
-// of the tile's steps, so dK / dV are stored, else added atomically.
+// Steps [i0, i1) of key tile kt of (batch, kv head) bhk, by one workgroup.  The workgroup's dK
+// (times scale) and dV for the tile's keys go to kdst / vdst (the tile's first key row, row
+// stride E): the outputs when these are all of the tile's steps, or the partial slot of the
+// range that cut the tile; with kv_atomic they are added into the outputs with float atomics.
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, bool whole) {
+DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
+                   float *vdst, bool kv_atomic) {
     constexpr int DH = D / 2;
     constexpr int NDT = D / 32;
 
@@ -255,6 +285,14 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kBM; };
     // Keys of the tile a step's dQ product must cover (causal: up to the step's last query).
     auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
+    // Where a step's dQ share goes: this tile's slot (deterministic), or the float32 dq by atomics.
+    const bool dq_atomic = a.dq_part == nullptr;
+    const int rf = slot_from(s, kt);
+    const int64_t slot0 = slot_before(s, kt) * ((int64_t)s.B * s.H);
+    auto dq_dst = [&](int bh, int m0) -> float * {
+        if (dq_atomic) return a.dq_acc + ((int64_t)bh * s.L + m0) * s.E;
+        return a.dq_part + (slot0 + (int64_t)bh * (s.L - rf) + (m0 - rf)) * s.E;
+    };
 
     QStage<D> stage;
     if (VEC && i0 < i1) {
@@ -268,8 +306,8 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
         __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
         if (prev_bh >= 0)
-            dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0),
-                          s.L, s.E, s.scale, wave, lane);
+            dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
+                          s.scale, wave, lane);
         if (VEC) {
             stage.store(sm, tid);
         } else {
@@ -340,10 +378,10 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     }
     __syncthreads();
     if (prev_bh >= 0)
-        dq_product<D>(sm, a.dq_acc + (int64_t)prev_bh * s.L * s.E, prev_m0, step_keys(prev_m0), s.L,
-                      s.E, s.scale, wave, lane);
+        dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
+                      wave, lane);
 
-    if (!whole) {
+    if (kv_atomic) {
         // A share of the tile's steps: dK and dV are added atomically.  Each wave's 32 x D block
         // goes through LDS first (the whole shared area is free after the last dQ product), so
         // that one atomic instruction covers consecutive dims of one key: straight from the
@@ -367,15 +405,15 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
                 if (d < s.E) unsafeAtomicAdd(dst + (int64_t)rr * s.E + d, blk[rr * RS + d]);
             }
         };
-        flush(dk, s.scale, static_cast<float *>(a.dk) + ((int64_t)bhk * s.S + kw0) * s.E);
-        flush(dv, 1.f, static_cast<float *>(a.dv) + ((int64_t)bhk * s.S + kw0) * s.E);
+        flush(dk, s.scale, kdst + (int64_t)(kw0 - n0) * s.E);
+        flush(dv, 1.f, vdst + (int64_t)(kw0 - n0) * s.E);
         return;
     }
 
     // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
     if (key < s.S) {
-        float *dkr = static_cast<float *>(a.dk) + ((int64_t)bhk * s.S + key) * s.E;
-        float *dvr = static_cast<float *>(a.dv) + ((int64_t)bhk * s.S + key) * s.E;
+        float *dkr = kdst + (int64_t)(key - n0) * s.E;
+        float *dvr = vdst + (int64_t)(key - n0) * s.E;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -404,7 +442,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     __shared__ BwdSmem<D> sm;
     const int BHk = a.s.B * a.s.Hkv;
     const int kt = blockIdx.x / BHk;  // tile 0 has the most causal work, so it goes first
-    key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, blockIdx.x % BHk, kt, 0, tile_steps(a.s, kt), true);
+    const int bhk = blockIdx.x % BHk;
+    const int64_t row0 = ((int64_t)bhk * a.s.S + (int64_t)kt * kBN) * a.s.E;
+    key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, 0, tile_steps(a.s, kt),
+                                   static_cast<float *>(a.dk) + row0, static_cast<float *>(a.dv) + row0, false);
+}
+
+// Where a stream-K range's share of a key tile it cuts goes: slot 0 of the range for the tile it
+// starts in, slot 1 for the tile it ends in (a range cuts at most these two); each slot holds a
+// whole tile's dK (times scale) then dV.
+DEVI float *kv_slot(const BwdArgs &a, int64_t range, int which) {
+    return a.kv_part + (range * 2 + which) * 2 * (int64_t)kBN * a.s.E;
 }
 
 // One workgroup per range of the stream-K schedule, ranges dealt to the 8 XCDs in contiguous
@@ -432,8 +480,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
         const int n = tile_steps(a.s, kt);
         const int i1 = (int)min((int64_t)n, i + (end - pos));
         if (!first) __syncthreads();  // the previous tile's last dQ product has read sm.kt, sm.ds
+        const bool whole = i == 0 && i1 == n;
+        const int64_t row0 = ((int64_t)bhk * a.s.S + (int64_t)kt * kBN) * a.s.E;
+        float *kd = static_cast<float *>(a.dk) + row0, *vd = static_cast<float *>(a.dv) + row0;
+        if (!whole && a.kv_part) {
+            kd = kv_slot(a, c, first ? 0 : 1);
+            vd = kd + (int64_t)kBN * a.s.E;
+        }
+        key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, kd, vd, !whole && !a.kv_part);
         first = false;
-        key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, i == 0 && i1 == n);
         pos += i1 - i;
         i = 0;
         do {
@@ -442,25 +497,105 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
     }
 }
 
-// The pre-kernel of the float32 backward: blocks below `rows_blocks` compute dsum and clear dQ
-// (bwd_pre_block); with a stream-K schedule each further block clears dK and dV of one key tile
-// that no single workgroup owns (split, or without steps: nobody writes it).
+// A key tile of the stream-K schedule: its first step's position and step count; `cut` when its
+// steps fall in more than one range (so no single workgroup stores its dK / dV).
+struct SkTile {
+    int64_t ts;
+    int n;
+    bool cut;
+};
+DEVI SkTile sk_tile(const AttnShape &s, const StreamK &sk, int bhk, int kt) {
+    int64_t ts = (int64_t)bhk * sk.per_kvh;
+    for (int k = 0; k < kt; ++k) ts += tile_steps(s, k);
+    const int n = tile_steps(s, kt);
+    return {ts, n, n > 0 && chunk_of(sk, ts) != chunk_of(sk, ts + n - 1)};
+}
+
+// The pre-kernel of the float32 backward: blocks below `rows_blocks` compute dsum and, without
+// the deterministic slots, clear the float32 dq its atomics accumulate into (bwd_pre_block);
+// in that case, with a stream-K schedule, each further block clears dK and dV of one key tile
+// that no single workgroup owns (cut, or without steps: nobody writes it).
 __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(BwdArgs a, StreamK sk, int rows_blocks) {
     if ((int)blockIdx.x < rows_blocks) {
-        bwd_pre_block<float, true>(a, blockIdx.x);
+        if (a.dq_part) bwd_pre_block<float, false>(a, blockIdx.x);
+        else bwd_pre_block<float, true>(a, blockIdx.x);
         return;
     }
     const AttnShape &s = a.s;
     const int nkt = (s.S + kBN - 1) / kBN;
     const int t = blockIdx.x - rows_blocks, bhk = t / nkt, kt = t % nkt;
-    int64_t ts = (int64_t)bhk * sk.per_kvh;
-    for (int k = 0; k < kt; ++k) ts += tile_steps(s, k);
-    const int n = tile_steps(s, kt);
-    if (n > 0 && chunk_of(sk, ts) == chunk_of(sk, ts + n - 1)) return;  // one owner stores it
+    const SkTile tile = sk_tile(s, sk, bhk, kt);
+    if (tile.n > 0 && !tile.cut) return;  // one owner stores it
     const int n0 = kt * kBN, n1 = min(s.S, n0 + kBN);
     const int64_t base = ((int64_t)bhk * s.S + n0) * s.E, count = (int64_t)(n1 - n0) * s.E;
     float *dk = static_cast<float *>(a.dk) + base, *dv = static_cast<float *>(a.dv) + base;
     for (int64_t j = threadIdx.x; j < count; j += 256) dk[j] = 0.f, dv[j] = 0.f;
+}
+
+// The reductions of the deterministic float32 backward.  Blocks below dq_blocks: dq = scale *
+// the sum of the key tiles' dQ slots in tile order, one thread per 4 dims of a row.  With a
+// stream-K schedule, each further block finishes one key tile: a cut tile's dK / dV are the sum
+// of its ranges' slots in range order; a tile without steps gets zeros; the others were stored
+// by their one workgroup.
+// vec4: E % 4 == 0 and dq 16-byte aligned (16-byte loads and stores).
+__global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK sk, int dq_blocks, bool vec4) {
+    const AttnShape &s = a.s;
+    const int nkt = (s.S + kBN - 1) / kBN;
+    const int BH = s.B * s.H;
+    if ((int)blockIdx.x < dq_blocks) {
+        const int c4 = (s.E + 3) / 4;
+        const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        if (t >= (int64_t)BH * s.L * c4) return;
+        const int64_t row = t / c4;
+        const int d0 = (int)(t % c4) * 4;
+        const int bh = (int)(row / s.L), r = (int)(row % s.L);
+        const int last = s.causal ? min(nkt - 1, r / kBN) : nkt - 1;  // tiles whose steps cover r
+        const bool vec = vec4;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        int64_t before = 0;  // slot_before(kt), accumulated
+        for (int kt = 0; kt <= last; ++kt) {
+            const int rf = slot_from(s, kt);
+            const float *src = a.dq_part + ((before * BH) + (int64_t)bh * (s.L - rf) + (r - rf)) * s.E + d0;
+            if (vec) {
+                acc += *reinterpret_cast<const f32x4 *>(src);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (d0 + e < s.E) acc[e] += src[e];
+            }
+            before += s.L - rf;
+        }
+        float *dst = static_cast<float *>(a.dq) + row * s.E + d0;
+        if (vec) {
+            *reinterpret_cast<f32x4 *>(dst) = acc * s.scale;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (d0 + e < s.E) dst[e] = acc[e] * s.scale;
+        }
+        return;
+    }
+    const int t = blockIdx.x - dq_blocks, bhk = t / nkt, kt = t % nkt;
+    const SkTile tile = sk_tile(s, sk, bhk, kt);
+    if (tile.n > 0 && !tile.cut) return;  // stored by its one workgroup
+    const int n0 = kt * kBN, n1 = min(s.S, n0 + kBN);
+    const int64_t base = ((int64_t)bhk * s.S + n0) * s.E, count = (int64_t)(n1 - n0) * s.E;
+    float *dk = static_cast<float *>(a.dk) + base, *dv = static_cast<float *>(a.dv) + base;
+    const int64_t c0 = tile.n > 0 ? chunk_of(sk, tile.ts) : 0, c1 = tile.n > 0 ? chunk_of(sk, tile.ts + tile.n - 1) : -1;
+    // Range c0 starts inside this tile (slot 0) unless it began in an earlier tile (slot 1); the
+    // later ranges all start inside it.  With more ranges than steps some ranges are empty: they
+    // wrote nothing and are skipped.
+    const bool c0_starts_here = c0 * sk.total / sk.chunks >= tile.ts;
+    for (int64_t j = threadIdx.x; j < count; j += 256) {
+        float sk_ = 0.f, sv = 0.f;
+        for (int64_t c = c0; c <= c1; ++c) {
+            if ((c + 1) * sk.total / sk.chunks == c * sk.total / sk.chunks) continue;  // empty range
+            const float *slot = kv_slot(a, c, (c == c0 && !c0_starts_here) ? 1 : 0);
+            sk_ += slot[j];
+            sv += slot[(int64_t)kBN * s.E + j];
+        }
+        dk[j] = sk_, dv[j] = sv;
+    }
 }
 
 // Workgroups of the backward that fit on the device at once (the occupancy the kernel's
@@ -476,14 +611,14 @@ int resident_workgroups(int D, bool mask) { return device_cus() * (D <= 64 && !m
 //     B6 H16 L1024 D64 (1.5 waves) 652 -> 548 us.
 // With at least as many causal tiles as slots, whole tiles dealt longest first keep the device
 // busy (a CU left with one workgroup runs it nearly twice as fast), and the cut tiles' extra
-// prologues, atomics and clearing cost 2-6%: B8 H12 L1024 376 -> 391 us, B16 H16 L1024 828 ->
+// prologues and partial dK / dV cost 2-6%: B8 H12 L1024 376 -> 391 us, B16 H16 L1024 828 ->
 // 879 us.  chunks == 0: whole tiles.
-StreamK plan_streamk(const AttnShape &s, int D) {
+StreamK plan_streamk(const AttnShape &s, int D, bool mask) {
     StreamK k{0, 0, 0};
     const int nkt = (s.S + kBN - 1) / kBN;
     for (int kt = 0; kt < nkt; ++kt) k.per_kvh += tile_steps(s, kt);
     k.total = k.per_kvh * s.B * s.Hkv;
-    const int slots = resident_workgroups(D, s.mask != nullptr) & ~7;
+    const int slots = resident_workgroups(D, mask) & ~7;
     if (slots < 8 || k.total == 0) return k;
     const int64_t tiles = (int64_t)nkt * s.B * s.Hkv;
     const int64_t last = tiles % slots;  // workgroups of the last, partial wave
@@ -492,6 +627,15 @@ StreamK plan_streamk(const AttnShape &s, int D) {
     if (underfilled || ragged) k.chunks = slots;
     return k;
 }
+
+// Bytes of the deterministic partials: the dQ slots of all key tiles, then two dK / dV slots per
+// stream-K range.
+size_t dq_part_bytes(const AttnShape &s) {
+    const int nkt = (s.S + kBN - 1) / kBN;
+    return (size_t)slot_before(s, nkt) * s.B * s.H * s.E * sizeof(float);
+}
+size_t kv_part_bytes(const StreamK &sk, int E) { return (size_t)sk.chunks * 4 * kBN * E * sizeof(float); }
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 template <int D, bool VEC>
 hipError_t launch_dv(const BwdArgs &a, const StreamK &sk, hipStream_t st) {
@@ -512,22 +656,49 @@ hipError_t launch_dv(const BwdArgs &a, const StreamK &sk, hipStream_t st) {
 }
 
 template <int D>
-hipError_t launch_d(const BwdArgs &args, hipStream_t st) {
+hipError_t launch_d(const BwdArgs &args, size_t part_bytes, hipStream_t st) {
     BwdArgs a = args;
     a.s.vec = args.s.vec && args.s.E == D;  // the ABI checked 16-byte alignment; E must fill D
-    const StreamK sk = plan_streamk(a.s, D);
+    const StreamK sk = plan_streamk(a.s, D, a.s.mask != nullptr);
     record_schedule(streamk_ranges, sk.chunks);
-    record_schedule(deterministic, 0);  // dQ (and cut tiles' dK / dV) by float atomics
+    // Deterministic when the workspace holds the slots; otherwise float atomics.
+    const size_t dq_bytes = align256(dq_part_bytes(a.s));
+    if (a.dq_part && dq_bytes + kv_part_bytes(sk, a.s.E) <= part_bytes) {
+        a.kv_part = sk.chunks > 0 ? a.dq_part + dq_bytes / sizeof(float) : nullptr;
+    } else {
+        a.dq_part = a.kv_part = nullptr;
+    }
+    record_schedule(deterministic, a.dq_part ? 1 : 0);
     const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
     const int rows_blocks = (int)((rows + 15) / 16);
-    const int64_t zero_blocks = sk.chunks > 0 ? (int64_t)a.s.B * a.s.Hkv * ((a.s.S + kBN - 1) / kBN) : 0;
+    const int64_t tiles = (int64_t)a.s.B * a.s.Hkv * ((a.s.S + kBN - 1) / kBN);
+    const int64_t zero_blocks = sk.chunks > 0 && !a.dq_part ? tiles : 0;
     if (rows_blocks + zero_blocks > 0)
         return_if(launch(bwd_pre_f32_kernel, dim3((unsigned)(rows_blocks + zero_blocks)), dim3(256), st, a, sk,
                          rows_blocks));
-    return a.s.vec ? launch_dv<D, true>(a, sk, st) : launch_dv<D, false>(a, sk, st);
+    return_if((a.s.vec ? launch_dv<D, true>(a, sk, st) : launch_dv<D, false>(a, sk, st)));
+    if (!a.dq_part) return hipSuccess;
+    const int64_t dq_threads = rows * ((a.s.E + 3) / 4);
+    const int dq_blocks = (int)((dq_threads + 255) / 256);
+    const int64_t reduce_blocks = dq_blocks + (sk.chunks > 0 ? tiles : 0);
+    const bool vec4 = args.s.vec && (a.s.E & 3) == 0;  // the ABI's s.vec: every pointer 16-byte aligned
+    return launch(bwd_reduce_f32_kernel, dim3((unsigned)reduce_blocks), dim3(256), st, a, sk, dq_blocks, vec4);
+}
+
+template <int D>
+size_t part_bytes_d(const AttnShape &s) {
+    const size_t kv = std::max(kv_part_bytes(plan_streamk(s, D, false), s.E), kv_part_bytes(plan_streamk(s, D, true), s.E));
+    return align256(dq_part_bytes(s)) + align256(kv);
 }
 
 }  // namespace
+
+size_t bwd_f32_part_bytes(const AttnShape &s) {
+    if (s.B * s.Hkv == 0 || s.S == 0 || s.L == 0) return 0;
+    if (s.E <= 32) return part_bytes_d<32>(s);
+    if (s.E <= 64) return part_bytes_d<64>(s);
+    return part_bytes_d<128>(s);
+}
 
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st) {
     if (a.s.B * a.s.Hkv == 0 || a.s.S == 0) {
@@ -535,9 +706,9 @@ hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st) {
         if (rows > 0) return launch(bwd_pre_kernel<float, true>, dim3((rows + 15) / 16), dim3(256), st, a);
         return hipSuccess;
     }
-    if (a.s.E <= 32) return launch_d<32>(a, st);
-    if (a.s.E <= 64) return launch_d<64>(a, st);
-    return launch_d<128>(a, st);
+    if (a.s.E <= 32) return launch_d<32>(a, a.part_bytes, st);
+    if (a.s.E <= 64) return launch_d<64>(a, a.part_bytes, st);
+    return launch_d<128>(a, a.part_bytes, st);
 }
 
 }  // namespace dc

@@ -48,6 +48,23 @@ DEVI bf16x8 cvt_f16x8(const f32x16 &x, int at) {
     return __builtin_bit_cast(bf16x8, h);
 }
 
+// The rounding error that cvt_f16x8(x, at) leaves, x[at + j] - hi[j], itself rounded to fp16:
+// hi + lo carries x to about 2^-22 of its magnitude.
+DEVI bf16x8 cvt_f16x8_lo(const f32x16 &x, int at, bf16x8 hi) {
+    const f16x8 h = __builtin_bit_cast(f16x8, hi);
+    f16x8 l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) l[j] = static_cast<_Float16>(x[at + j] - static_cast<float>(h[j]));
+    return __builtin_bit_cast(bf16x8, l);
+}
+// True in every lane when any lane's x[at .. at + 7] exceeds `t` (one wave-wide vote).
+DEVI bool any_above(const f32x16 &x, int at, float t) {
+    float m = x[at];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) m = fmaxf(m, x[at + j]);
+    return __builtin_amdgcn_ballot_w64(m > t) != 0;
+}
+
 // Row index (within a 32-row MFMA tile) that accumulator register r of this lane holds.
 DEVI int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 

@@ -53,6 +53,12 @@ struct BwdArgs {
     void *dq, *dk, *dv;
     float *dsum;    // (B, H, L) workspace: rowsum(dout * out)
     float *dq_acc;  // (B, H, L, E) float32 accumulator (== dq for float32)
+    // float32, deterministic (when the workspace holds them): each key tile's dQ share goes to a
+    // slot of its own (the rows its steps cover), summed in tile order by a reduction; tiles the
+    // stream-K schedule cuts between ranges leave each range's dK / dV share in that range's
+    // slot, summed in range order.  nullptr: float atomics into dq (and dk / dv of cut tiles).
+    float *dq_part, *kv_part;
+    size_t part_bytes;  // workspace bytes at dq_part
     // bf16: q, k, v, dout copied to fp16 (f16_stage.hip), each scaled by 2^e per (b, kv head)
     // (q and dout per group of query heads sharing a kv head); exps holds e_q, e_k, e_v, e_do,
     // B*Hkv each.  nullptr: P and dS enter their products as bf16 hi + lo.
@@ -109,6 +115,9 @@ hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st);
 // The same for the bf16 forward (its unmasked path with the fp16 copy of V).
 size_t fwd_bf16_split_bytes(const AttnShape &s);
 hipError_t launch_bwd_f32(const BwdArgs &a, hipStream_t st);
+// Workspace bytes of the float32 backward's deterministic partials on the current device (dQ
+// slots, then the stream-K cut tiles' dK / dV slots), with or without a mask.
+size_t bwd_f32_part_bytes(const AttnShape &s);
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st);
 // Workspace bytes the bf16 backward uses to split its grids on the current device (0: it does not
 // split this shape).

@@ -81,10 +81,14 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
 
 /* Backward (dq, dk, dv) from the saved out and lse.  src/lib.rs:640-683,
  * src/torch_attention.rs:286-468.  The workspace must hold dsum (batch * heads * q_len floats);
- * the size returned also covers, for bf16, scaled fp16 copies of q, k, v and grad_out (with
- * less, P and dS enter their products as bf16 hi + lo pairs) and, for bf16 without a mask on
- * grids that fill at most half of the current device, the float32 partials of its split grids
- * (so the size depends on the device current at the call). */
+ * the size returned also covers, for float32, the partials that make the result identical from
+ * run to run (each key tile's dQ share, and on few-tile grids the dK / dV shares of key tiles
+ * split between workgroups, summed in a fixed order; with less, these shares are added with
+ * float atomics and the last bits of dq, dk, dv can vary between runs), for bf16, scaled fp16
+ * copies of q, k, v and grad_out (with less, P and dS enter their products as bf16 hi + lo
+ * pairs) and, for bf16 without a mask on grids that fill at most half of the current device,
+ * the float32 partials of its split grids.  The size depends on the device current at the call
+ * (its compute-unit count sets the few-tile schedules). */
 size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q, const void *k,
                       const void *v, const void *out, const float *lse, const float *mask,

@@ -140,15 +140,18 @@ def test_mask_strides_and_workspace_checks():
     assert "mask must be (B, H, L, S)" in L.dc_last_error().decode()
     d = desc()
     need = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
-    assert need >= 2 * 4 * 8 * 4  # dsum, float32 per (b, h, l)
-    st = L.dc_sdpa_bwd(ctypes.byref(d), *([None] * 11), need - 1, None)
+    dsum = 256  # the minimum: dsum, float32 per (b, h, l) = 2 * 4 * 8 * 4 bytes, 256-byte aligned
+    # float32 asks for dsum plus the deterministic dQ slots (one key tile: 8 rows of each of the
+    # 8 (b, h), 16 floats each); with only dsum it still runs (dQ by float atomics).
+    assert need >= dsum + 8 * 8 * 16 * 4
+    st = L.dc_sdpa_bwd(ctypes.byref(d), *([None] * 11), dsum - 1, None)
     assert st == _lib.DC_INVALID_ARGUMENT and "workspace" in L.dc_last_error().decode()
     bf = desc(dtype=_lib.DC_BF16)
     # bf16 asks for dsum plus the fp16 copies of q, k, v, dout (B2 H4 L8 E16: 2 x 1024 + 2 x 512
     # halves) and their scratch; with only dsum it still runs (the bf16 hi + lo products).
     need_bf = L.dc_sdpa_bwd_workspace_size(ctypes.byref(bf))
-    assert need_bf >= need + 2 * (2 * 4 * 8 * 16) * 2 + 2 * (2 * 2 * 8 * 16) * 2
-    st = L.dc_sdpa_bwd(ctypes.byref(bf), *([None] * 11), need - 1, None)
+    assert need_bf >= dsum + 2 * (2 * 4 * 8 * 16) * 2 + 2 * (2 * 2 * 8 * 16) * 2
+    st = L.dc_sdpa_bwd(ctypes.byref(bf), *([None] * 11), dsum - 1, None)
     assert st == _lib.DC_INVALID_ARGUMENT and "workspace" in L.dc_last_error().decode()
     fw = L.dc_sdpa_fwd_workspace_size(ctypes.byref(bf))
     assert fw >= L.dc_sdpa_fwd_workspace_size(ctypes.byref(d)) + 2 * 2 * 8 * 16 * 2  # + V's fp16 copy

@@ -1,0 +1,97 @@
+"""Bit-reproducibility of the float32 backward (the reference's guarantee that the thread split never
+changes the bits, src/torch_attention.rs:8).
+
+With the full workspace (dc_sdpa_bwd_workspace_size) the float32 backward uses no float atomics:
+each key tile's dQ share goes to a slot of its own and a reduction sums the slots in tile order;
+key tiles the stream-K schedule cuts between ranges leave each range's dK / dV share in that
+range's slot, summed in range order.  Each case runs the backward three times through the C ABI
+with the workspace and the outputs filled with NaN before every call (a slot read before it is
+written, or an output element nobody writes, would show up as NaN), checks that the three runs are
+bit-identical, that the schedule query reports the schedule the case is meant to take, and that
+the results meet the float32 bar against the oracle: |gpu - ref| <= 2e-5 + 1e-5 |ref|.
+"""
+import numpy as np
+import pytest
+
+from tests._data import assert_f32
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _backward_poisoned(g, q, k, v, out, lse, causal, mask):
+    from densecore_amd import _lib, _native
+    dims = _native._attention_dims(q, k, v)
+    B, H, Hkv, L, S, E = dims
+    m, ms = _native._mask_arg(mask, dims, q.device)
+    d = _native._desc(dims, causal, None, torch.float32, ms)
+    L_ = _lib.lib()
+    nbytes = L_.dc_sdpa_bwd_workspace_size(d)
+    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=DEV)
+    sched = _native._schedule(True, q, k, v, causal, mask=m, workspace_bytes=nbytes)
+    runs = []
+    for _ in range(3):
+        ws.fill_(float("nan"))
+        dq = torch.full((B, H, L, E), float("nan"), device=DEV)
+        dk = torch.full((B, Hkv, S, E), float("nan"), device=DEV)
+        dv = torch.full((B, Hkv, S, E), float("nan"), device=DEV)
+        _lib.check(L_.dc_sdpa_bwd(d, _native._ptr(g), _native._ptr(q), _native._ptr(k), _native._ptr(v),
+                                  _native._ptr(out), _native._ptr(lse), _native._ptr(m), _native._ptr(dq),
+                                  _native._ptr(dk), _native._ptr(dv), _native._ptr(ws), nbytes,
+                                  _native._stream(q.device)))
+        torch.cuda.synchronize()
+        runs.append((dq, dk, dv))
+    return runs, sched
+
+
+CASES = [  # tag, B, H, Hkv, L, S, E, causal, mask, stream-K expected
+    ("c2_whole", 8, 12, 12, 1024, 1024, 64, True, None, False),
+    ("streamk_causal", 1, 8, 8, 2048, 2048, 64, True, None, True),
+    ("streamk_grouped", 2, 8, 2, 640, 640, 64, True, None, True),
+    ("streamk_more_ranges_than_steps", 1, 4, 4, 300, 700, 64, True, None, True),
+    ("streamk_ragged_noncausal", 6, 16, 16, 1024, 1024, 32, False, None, True),
+    ("streamk_masked", 1, 2, 2, 384, 384, 64, True, "float", True),
+    ("whole_e128_unaligned", 2, 16, 16, 1000, 900, 100, False, None, False),
+    ("whole_l_gt_s", 16, 16, 16, 1024, 260, 32, True, None, False),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal,mask,streamk", CASES, ids=[c[0] for c in CASES])
+def test_f32_backward_bit_reproducible(oracle_lib, tag, B, H, Hkv, L, S, E, causal, mask, streamk):
+    rng = np.random.default_rng(sum(map(ord, tag)) + 11)
+    q = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    g = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    mk = None
+    if mask == "float":
+        mk = rng.standard_normal((B, H, L, S), dtype=np.float32)
+        mk[rng.random((B, H, L, S)) < 0.2] = -np.inf
+    print(f"[case] f32 determinism {tag} B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, None, mk)
+    runs, sched = _backward_poisoned(_t(g), _t(q), _t(k), _t(v), _t(ref_o), _t(ref_l), causal,
+                                     None if mk is None else _t(mk))
+    print(f"[schedule] {sched}", flush=True)
+    assert sched["deterministic"] == 1, sched
+    assert (sched["streamk_ranges"] > 0) == streamk, sched
+    for name, a, b, c in zip(("dq", "dk", "dv"), *runs):
+        assert torch.equal(a, b) and torch.equal(a, c), f"{tag} {name}: runs differ"
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal, None, mk)
+    for name, a, r in zip(("dq", "dk", "dv"), runs[0], ref):
+        assert_f32(a.cpu().numpy(), r, f"{tag} {name}")
+
+
+def test_f32_backward_minimum_workspace_uses_atomics():
+    """With only dsum in the workspace the float32 backward falls back to float atomics (results
+    still meet the bar: covered by the schedule tests); the schedule query says so."""
+    from densecore_amd import _native
+    q = torch.zeros((1, 8, 2048, 64), device=DEV)
+    dsum = (8 * 2048 * 4 + 255) // 256 * 256
+    assert _native._schedule(True, q, q, q, True, workspace_bytes=dsum)["deterministic"] == 0
+    assert _native._schedule(True, q, q, q, True)["deterministic"] == 1
