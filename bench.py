@@ -228,8 +228,8 @@ def bench_math(torch, steps, warmup, dev):
     with dropout p = 0.1: softmax forward (scores + broadcast mask -> probabilities, 8 B per
     score) and backward (12 B per score) against HBM, the Bernoulli mask drawn from the
     reference's generator stream (draws/s), the dropout product (8 B per score plus the bits),
-    and one whole math-path step (forward + backward through autograd, the two batched
-    products on the device BLAS)."""
+    the two batched products (dc_bmm, next to the device BLAS), and one whole math-path step
+    (forward + backward through autograd, every product on dc_bmm)."""
     import densecore_amd._native as native
     from densecore_amd import functional as F, random as R
     from tests._data import CONFIGS, additive, make_inputs
@@ -264,6 +264,24 @@ def bench_math(torch, steps, warmup, dev):
     res["dropout_apply"] = {"ms": round(ms, 4), "gbps": round(nb / (ms * 1e-3) / 1e9, 1),
                             "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
     del x, y, g, bits
+    # The two batched products of the math path at C3's shape (256 (batch, head) items):
+    # scores = q k^T (k^T a transposed view, 512 x 64 x 512) and weights v (512 x 512 x 64), by
+    # dc_bmm and, for comparison, by the device BLAS (torch.bmm -> hipBLASLt).
+    qa, ka = torch.randn(B * H, L, E, device=dev), torch.randn(B * H, S, E, device=dev)
+    wa, va = torch.randn(B * H, L, S, device=dev), torch.randn(B * H, S, E, device=dev)
+    work = 2.0 * B * H * L * S * E
+    res["bmm"] = {"note": "TFLOP/s of 2*m*n*k per product, HIP events around back-to-back calls"}
+    for name, fn, ref in (("q_kT", lambda: native._bmm(qa, ka.transpose(1, 2)),
+                           lambda: torch.bmm(qa, ka.transpose(1, 2))),
+                          ("weights_v", lambda: native._bmm(wa, va), lambda: torch.bmm(wa, va))):
+        fn(), ref()
+        ms_dc = kernel_ms(torch, stream, fn, reps)
+        ms_bl = kernel_ms(torch, stream, ref, reps)
+        res["bmm"][name] = {"dc_bmm_ms": round(ms_dc, 4), "dc_bmm_tflops": round(work / (ms_dc * 1e-3) / 1e12, 2),
+                            "hipblaslt_ms": round(ms_bl, 4),
+                            "hipblaslt_tflops": round(work / (ms_bl * 1e-3) / 1e12, 2),
+                            "frac_fp32_mfma": round(work / (ms_dc * 1e-3) / 1e12 / PEAK_FP32_MFMA, 4)}
+    del qa, ka, wa, va
     q, k, v = (torch.from_numpy(d[c]).to(dev).requires_grad_(True) for c in "qkv")
     am = torch.from_numpy(d["mask_bool"]).to(dev)
     go = torch.randn((B, H, L, E), device=dev)

@@ -18,7 +18,7 @@ EXPORTS = ("dc_abi_version", "dc_last_error",
            "dc_sdpa_bwd_workspace_size", "dc_sdpa_bwd",
            "dc_sdpa_decode_workspace_size", "dc_sdpa_decode",
            "dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule", "dc_sdpa_decode_noalloc",
-           "dc_softmax_fwd", "dc_softmax_bwd",
+           "dc_bmm", "dc_softmax_fwd", "dc_softmax_bwd",
            "dc_mt19937_seed", "dc_mt19937_advance", "dc_mt19937_table_bytes",
            "dc_mt19937_table_init", "dc_bernoulli_max_draws", "dc_bernoulli_workspace_size",
            "dc_bernoulli", "dc_dropout_apply")
@@ -44,6 +44,14 @@ class Schedule(ctypes.Structure):
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+
+
+class BmmDesc(ctypes.Structure):
+    """``dc_bmm_desc``."""
+    _fields_ = [("batch", ctypes.c_int64), ("m", ctypes.c_int64), ("n", ctypes.c_int64),
+                ("k", ctypes.c_int64), ("a_stride_batch", ctypes.c_int64), ("a_stride_m", ctypes.c_int64),
+                ("a_stride_k", ctypes.c_int64), ("b_stride_batch", ctypes.c_int64),
+                ("b_stride_k", ctypes.c_int64), ("b_stride_n", ctypes.c_int64)]
 
 
 class SoftmaxDesc(ctypes.Structure):
@@ -80,6 +88,8 @@ def lib():
         for name in ("dc_sdpa_fwd_schedule", "dc_sdpa_bwd_schedule"):
             getattr(L, name).argtypes = [D, ctypes.c_int, SZ, ctypes.POINTER(Schedule)]
             getattr(L, name).restype = ctypes.c_int
+        L.dc_bmm.argtypes = [ctypes.POINTER(BmmDesc), P, P, P, P]
+        L.dc_bmm.restype = ctypes.c_int
         SD = ctypes.POINTER(SoftmaxDesc)
         L.dc_softmax_fwd.argtypes = [SD, P, P, P, P]
         L.dc_softmax_bwd.argtypes = [SD, P, P, P, P]

@@ -166,6 +166,28 @@ def _flash_decode(q, k, v, scale=None):
     return out, lse
 
 
+def _bmm(a, b):
+    """``bmm`` (``src/batched_matmul.rs:9-49``): (batch, m, k) x (batch, k, n) -> (batch, m, n),
+    float32, with the reference's shape errors.  The operands are read through their strides (a
+    transposed view is not copied); the result is a fresh contiguous tensor."""
+    if a.dim() != 3 or b.dim() != 3:
+        raise ValueError("bmm requires rank-3 operands")
+    if a.shape[0] != b.shape[0] or a.shape[2] != b.shape[1]:
+        raise ValueError("bmm batch or inner dimensions mismatch")
+    if a.device.type != "cuda" or b.device != a.device:
+        raise ValueError("bmm takes tensors on one GPU")
+    if a.dtype != torch.float32 or b.dtype != torch.float32:
+        raise ValueError("no registered bmm kernel for device/dtype")
+    batch, m, k = a.shape
+    n = b.shape[2]
+    c = torch.empty((batch, m, n), dtype=torch.float32, device=a.device)
+    sa, sb = a.stride(), b.stride()
+    d = _lib.BmmDesc(batch, m, n, k, sa[0], sa[1], sa[2], sb[0], sb[1], sb[2])
+    # A data pointer of an empty tensor may be anything: the library reads nothing then.
+    _lib.check(_lib.lib().dc_bmm(d, _ptr(a), _ptr(b), _ptr(c), _stream(a.device)))
+    return c
+
+
 def _softmax_desc(rows, width, heads=1, q_len=1, mstrides=(0, 0, 0), safe=False):
     return _lib.SoftmaxDesc(int(rows), int(width), int(heads), int(q_len), *map(int, mstrides),
                             int(bool(safe)), 0)

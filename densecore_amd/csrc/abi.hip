@@ -475,6 +475,26 @@ dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const voi
     return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
 }
 
+dc_status dc_bmm(const dc_bmm_desc *d, const float *a, const float *b, float *c, void *stream) {
+    if (d == nullptr) return fail(DC_INVALID_ARGUMENT, "bmm descriptor is null");
+    const int64_t dims[4] = {d->batch, d->m, d->n, d->k};
+    for (int64_t x : dims)
+        if (x < 0) return fail(DC_INVALID_ARGUMENT, "bmm requires rank-3 operands");
+    for (int64_t x : dims)
+        if (x > INT32_MAX) return fail(DC_UNSUPPORTED, "bmm dimension exceeds 2^31 - 1");
+    const int64_t tiles = ((d->m + 127) / 128) * ((d->n + 63) / 64) * d->batch;
+    if (tiles > INT32_MAX) return fail(DC_UNSUPPORTED, "bmm has more than 2^31 - 1 output tiles");
+    if (d->batch == 0 || d->m == 0 || d->n == 0) return ok();
+    if (c == nullptr || (d->k > 0 && (a == nullptr || b == nullptr)))
+        return fail(DC_INVALID_ARGUMENT, "bmm got a null pointer for a non-empty tensor");
+    dc::BmmArgs g{};
+    g.a = a, g.b = b, g.c = c;
+    g.batch = (int)d->batch, g.m = (int)d->m, g.n = (int)d->n, g.k = (int)d->k;
+    g.sab = d->a_stride_batch, g.sam = d->a_stride_m, g.sak = d->a_stride_k;
+    g.sbb = d->b_stride_batch, g.sbk = d->b_stride_k, g.sbn = d->b_stride_n;
+    return launched(dc::launch_bmm(g, static_cast<hipStream_t>(stream)));
+}
+
 dc_status dc_softmax_fwd(const dc_softmax_desc *d, const float *x, const float *mask, float *y,
                          void *stream) {
     dc::SoftmaxArgs a;

@@ -96,6 +96,17 @@ struct SoftmaxArgs {
     bool safe;
 };
 
+// Batched float32 matrix product (bmm.hip): C[b] = A[b] B[b], A (batch, m, k) and B (batch, k, n)
+// through element strides, C contiguous (batch, m, n).
+struct BmmArgs {
+    const float *a, *b;
+    float *c;
+    int batch, m, n, k;
+    int64_t sab, sam, sak;  // A's strides: batch, m, k
+    int64_t sbb, sbk, sbn;  // B's strides: batch, k, n
+};
+hipError_t launch_bmm(const BmmArgs &g, hipStream_t st);
+
 // Compute units of the current device, and workgroups of `kernel` (`threads` per workgroup) that
 // fit on one of them; both looked up once per device (and kernel) and cached.  0 if unknown.
 int device_cus();

@@ -9,10 +9,12 @@ saves (q, k, v, out, lse) for the backward.
 
 Inputs the flash path does not take (dropout, rank 3, Ev != E, masks the flash path rejects,
 float masks that require a gradient) go through the reference's math path
-(``functional.py:318-340``), composed on the device: the two batched products are the device
-BLAS (``torch.matmul``), the mask add, safe softmax and its gradient are this library's
-softmax kernels (``include/dc_math.h``).  ``multi_head_attention_forward``
-(``functional.py:400-461``) composes the same pieces.
+(``functional.py:318-340``), composed on the device from this library's kernels
+(``include/dc_math.h``): the two batched products are ``dc_bmm`` (the device entry of the
+reference's bmm registry, ``src/batched_matmul.rs:28-49``, with its gradient as two more bmm
+calls on transposed views), the mask add, safe softmax and its gradient are the softmax
+kernels.  ``multi_head_attention_forward`` (``functional.py:400-461``) composes the same pieces
+around its input and output projections.
 
 Differences, all on the device side of the boundary:
   * tensors are ``torch`` tensors on the GPU, float32 or bfloat16 (bf16 is new: the reference
@@ -87,7 +89,7 @@ def _math_attention(query, key, value, attn_mask, dropout_p, is_causal, scale):
         raise ValueError("attention tensors must be on one GPU")
     factor = math.sqrt(abs(scale))
     q = query * float(-factor if scale < 0 else factor)
-    attn = torch.matmul(q, (key * float(factor)).transpose(-2, -1))
+    attn = _matmul(q, (key * float(factor)).transpose(-2, -1))
     length, source = attn.shape[-2], attn.shape[-1]
     if is_causal:
         attn_mask = torch.ones((length, source), dtype=torch.bool, device=attn.device).tril()
@@ -105,7 +107,40 @@ def _math_attention(query, key, value, attn_mask, dropout_p, is_causal, scale):
     weights = softmax_masked(attn, additive, safe=additive is not None)
     if dropout_p:
         weights = dropout(weights, dropout_p, True)
-    return torch.matmul(weights, value)
+    return _matmul(weights, value)
+
+
+class _Bmm(torch.autograd.Function):
+    """``bmm`` with its gradient: dA = dC B^T and dB = A^T dC, both ``dc_bmm`` on transposed
+    views (no copies)."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return _native._bmm(a, b)
+
+    @staticmethod
+    def backward(ctx, grad):
+        a, b = ctx.saved_tensors
+        da = _native._bmm(grad, b.transpose(1, 2)) if ctx.needs_input_grad[0] else None
+        db = _native._bmm(a.transpose(1, 2), grad) if ctx.needs_input_grad[1] else None
+        return da, db
+
+
+def bmm(a, b):
+    """The reference's ``bmm`` (``src/batched_matmul.rs:9-49``) on float32 GPU tensors:
+    (batch, m, k) x (batch, k, n) -> (batch, m, n), strided operands, autograd."""
+    return _Bmm.apply(a, b)
+
+
+def _matmul(x, y):
+    """x @ y for x (..., m, k) and y (..., k, n) with equal leading dimensions (rank 3 or 4), as
+    one ``bmm`` over the flattened leading dimensions."""
+    lead = tuple(x.shape[:-2])
+    if tuple(y.shape[:-2]) != lead:
+        raise ValueError("bmm batch or inner dimensions mismatch")
+    out = bmm(x.reshape((-1,) + tuple(x.shape[-2:])), y.reshape((-1,) + tuple(y.shape[-2:])))
+    return out.reshape(lead + tuple(out.shape[-2:]))
 
 
 class _Softmax(torch.autograd.Function):
@@ -273,9 +308,10 @@ def multi_head_attention_forward(query, key, value, embed_dim_to_check, num_head
                                  static_v=None, average_attn_weights=True, is_causal=False):
     """PyTorch's reference algorithm as ``functional.py:400-461`` composes it, on the GPU.
     Inputs are (L, N, E), or (L, E) unbatched.  ``is_causal`` is only a hint: ``attn_mask``
-    must still be given and is the one applied.  The projections and the two batched products
-    are device BLAS calls; the mask add and softmax (no safe rows here, as in the reference) are
-    this library's softmax kernel, and dropout its dropout."""
+    must still be given and is the one applied.  The input and output projections are device
+    BLAS calls (``F.linear``); the two batched products are this library's ``bmm``, the mask add
+    and softmax (no safe rows here, as in the reference) its softmax kernel, and dropout its
+    dropout."""
     F = torch.nn.functional
     if is_causal and attn_mask is None:
         raise RuntimeError("Need attn_mask if specifying the is_causal hint")
@@ -314,11 +350,11 @@ def multi_head_attention_forward(query, key, value, embed_dim_to_check, num_head
         padding = key_padding_mask.reshape(bsz, 1, 1, src_len).expand(bsz, num_heads, 1, src_len)
         padding = padding.reshape(bsz * num_heads, 1, src_len)
         attn_mask = padding if attn_mask is None else attn_mask + padding
-    scores = torch.bmm(q * math.sqrt(1.0 / head_dim), k.transpose(1, 2).contiguous())
+    scores = bmm(q * math.sqrt(1.0 / head_dim), k.transpose(1, 2))
     probabilities = softmax_masked(scores, attn_mask, safe=False)
     if training and dropout_p > 0:
         probabilities = dropout(probabilities, dropout_p, True)
-    out = torch.bmm(probabilities, v).transpose(0, 1).reshape(tgt_len * bsz, embed_dim)
+    out = bmm(probabilities, v).transpose(0, 1).reshape(tgt_len * bsz, embed_dim)
     out = F.linear(out, out_proj_weight, out_proj_bias).reshape(tgt_len, bsz, -1)
     if not batched:
         out = out.squeeze(1)

@@ -5,9 +5,11 @@
  * The reference's math path (python/densecore/functional.py:318-340, used for dropout, masks
  * the flash path rejects, Ev != E and masks that require a gradient) and its
  * multi_head_attention_forward (functional.py:400-461) are composed from bmm, an additive
- * mask, softmax over the last axis and dropout.  The two products are plain batched GEMMs (the
- * caller's BLAS); this header covers the rest:
+ * mask, softmax over the last axis and dropout.  This header covers each of them:
  *
+ *   dc_bmm           replaces  the (Cpu, Float32) entry of the bmm registry
+ *                              src/batched_matmul.rs:28-49 -> torch_blas::bmm src/torch_blas.rs:404-449
+ *                    (a device entry of that table: strided (batch, m, k) x (batch, k, n))
  *   dc_softmax_fwd   replaces  Tensor.softmax(-1) on the scores   src/lib.rs:269-270
  *                              -> activation_dispatch::softmax     src/activation_dispatch.rs:61
  *                              -> torch_softmax::softmax_lastdim   src/torch_softmax.rs:57-67
@@ -39,6 +41,18 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* C[b] = A[b] B[b] in float32.  A is (batch, m, k), B is (batch, k, n), each read through its
+ * element strides (a transposed view is other strides; any layout is accepted, the fastest have
+ * a stride of 1 along m, n or k with 16-byte aligned rows); C is contiguous (batch, m, n).  k == 0
+ * gives zeros (src/batched_matmul.rs:63-65).  Sizes above 2^31 - 1 are DC_UNSUPPORTED. */
+typedef struct {
+    int64_t batch, m, n, k;
+    int64_t a_stride_batch, a_stride_m, a_stride_k;
+    int64_t b_stride_batch, b_stride_k, b_stride_n;
+} dc_bmm_desc;
+
+dc_status dc_bmm(const dc_bmm_desc *d, const float *a, const float *b, float *c, void *stream);
 
 typedef struct {
     int64_t rows, width;

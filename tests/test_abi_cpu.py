@@ -207,3 +207,33 @@ def test_schedule_query_is_a_dry_run():
     bad = _lib.Desc(1, 3, 2, 4, 4, 8, 0, 0, 0.0, _lib.DC_F32, 0, 0, 0, 0)
     assert L.dc_sdpa_fwd_schedule(ctypes.byref(bad), 0, 0, ctypes.byref(out)) == _lib.DC_INVALID_ARGUMENT
     assert L.dc_last_error() == b"flash attention q/k/v shapes do not match"
+
+
+def test_bmm_argument_errors():
+    """dc_bmm rejects bad shapes before any launch (no GPU needed)."""
+    L = _lib.lib()
+
+    def bmm(batch, m, n, k, a=None, b=None, c=None):
+        d = _lib.BmmDesc(batch, m, n, k, m * k, k, 1, k * n, n, 1)
+        return L.dc_bmm(ctypes.byref(d), a, b, c, None)
+
+    assert bmm(-1, 2, 2, 2) == _lib.DC_INVALID_ARGUMENT
+    assert L.dc_last_error() == b"bmm requires rank-3 operands"
+    assert bmm(1, 2 ** 31, 2, 2) == _lib.DC_UNSUPPORTED
+    assert bmm(0, 5, 5, 5) == _lib.DC_OK  # nothing to compute: no pointers needed
+    assert bmm(3, 0, 5, 5) == _lib.DC_OK
+    assert bmm(2, 3, 4, 5) == _lib.DC_INVALID_ARGUMENT
+    assert b"null pointer" in L.dc_last_error()
+
+
+def test_bmm_descriptor_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "dc_math.h"\n'
+                   "int main(void){printf(\"%zu %zu %zu\\n\", sizeof(dc_bmm_desc),"
+                   " offsetof(dc_bmm_desc, a_stride_batch), offsetof(dc_bmm_desc, b_stride_n));return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True,
+                                       check=True).stdout.split()))
+    D = _lib.BmmDesc
+    assert got == [ctypes.sizeof(D), D.a_stride_batch.offset, D.b_stride_n.offset]

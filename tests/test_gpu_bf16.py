@@ -263,3 +263,39 @@ def test_bf16_without_fp16_copies(oracle_lib):
                               ws.data_ptr(), ws.numel(), stream))
     for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
         assert_bf16(_np(a), r, name)
+
+
+def test_bf16_long_causal_early_keys():
+    """dV and dK of the first keys of a long causal row.  Key j < 64 is seen by every later query,
+    the nearby ones with P ~ 1 / (query + 1): thousands of terms, the large ones of either sign,
+    cancel to a small sum.  P and dS rounded once to fp16 (2^-12 per term) left errors of ~1% of
+    rms(dV) there at L = 8192; blocks with large P now also carry the rounding error.  Checked
+    against float64 (P from the GPU's lse, dsum from its bf16 out, as the backward takes them):
+    |gpu - ref| <= 2^-7 |ref| + 3e-4 rms(ref), i.e. twice the outputs' own bf16 rounding (up to
+    2^-8 |ref|) plus a small allowance.  A float64 emulation of these inputs gives 0.49 (dV) and
+    0.63 (dK) of this bound for the kernels' products, 1.59 and 1.84 for fp16-only products."""
+    from densecore_amd import _native
+    B, H, L, E = 1, 1, 8192, 128
+    rng = np.random.default_rng(8192)
+    q, k, v, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(4))
+    print("[case] bf16 causal L8192 D128 early keys vs float64", flush=True)
+    tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
+    out, lse = _native._flash_attention(tq, tk, tv, True)
+    dq, dk, dv = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, True)
+    torch.cuda.synchronize()
+    o, l = _np(out)[0, 0].astype(np.float64), lse.cpu().numpy()[0, 0].astype(np.float64)
+    q64, k64, v64, g64 = (x[0, 0].astype(np.float64) for x in (q, k, v, g))
+    scale = 1.0 / np.sqrt(E)
+    J = 64
+    s = q64 @ k64[:J].T * scale                              # (L, J): every query, the first keys
+    s[np.arange(L)[:, None] < np.arange(J)[None, :]] = -np.inf
+    p = np.exp(s - l[:, None])
+    dsum = np.sum(g64 * o, axis=1)
+    ds = p * (g64 @ v64[:J].T - dsum[:, None])
+    ref = {"dv": p.T @ g64, "dk": scale * (ds.T @ q64)}
+    got = {"dv": _np(dv)[0, 0, :J], "dk": _np(dk)[0, 0, :J]}
+    for name in ("dv", "dk"):
+        r = ref[name]
+        bar = 2.0 ** -7 * np.abs(r) + 3e-4 * np.sqrt(np.mean(r ** 2))
+        err = np.abs(got[name] - r)
+        assert np.all(err <= bar), f"{name}: max err / bar {np.max(err / bar):.3f}"

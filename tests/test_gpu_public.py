@@ -18,7 +18,8 @@ k.grad, v.grad against the oracle run the way the reference runs them:
     |gpu - ref| <= 1e-2 |ref| + 1e-2 rms(ref).
 
 Every case asserts that the flash branch ran: ``out.grad_fn`` is the flash autograd node, and
-the math path and the device BLAS (``torch.matmul`` / ``torch.bmm``) are never entered.
+the math path, its batched products (``dc_bmm``) and the device BLAS (``torch.matmul`` /
+``torch.bmm``) are never entered.
 """
 import numpy as np
 import pytest
@@ -40,6 +41,7 @@ def flash_only(monkeypatch):
         raise AssertionError("the math path / device BLAS ran instead of the flash kernels")
 
     monkeypatch.setattr(F, "_math_attention", boom)
+    monkeypatch.setattr(F._native, "_bmm", boom)
     monkeypatch.setattr(torch, "matmul", boom)
     monkeypatch.setattr(torch, "bmm", boom)
     return F
