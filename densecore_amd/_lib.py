@@ -39,11 +39,11 @@ class Schedule(ctypes.Structure):
     _fields_ = [("split_chunk", ctypes.c_int32), ("split_pieces", ctypes.c_int32),
                 ("streamk_ranges", ctypes.c_int32), ("split_chunk_k", ctypes.c_int32),
                 ("split_chunk_q", ctypes.c_int32), ("f16_products", ctypes.c_int32),
-                ("deterministic", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("deterministic", ctypes.c_int32), ("materialized_rows", ctypes.c_int32),
                 ("workgroups", ctypes.c_int64)]
 
     def as_dict(self):
-        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 class BmmDesc(ctypes.Structure):

@@ -94,8 +94,6 @@ dc_status check_dims(const dc_attn_desc *d, dc::AttnShape *s) {
             return fail(DC_UNSUPPORTED, "flash attention dimension exceeds 2^31 - 1");
     if (d->batch * d->heads > INT32_MAX / 2 || d->batch * d->kv_heads > INT32_MAX / 2)
         return fail(DC_UNSUPPORTED, "flash attention batch * heads exceeds 2^30");
-    if (d->head_dim > 128)
-        return fail(DC_UNSUPPORTED, "flash attention head_dim above 128 is not implemented");
     s->B = (int)d->batch;
     s->H = (int)d->heads;
     s->Hkv = (int)d->kv_heads;
@@ -141,6 +139,7 @@ size_t fwd_partial_ws(const dc::AttnShape &s) {
 }
 size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
+    if (s.E > dc::kFlashMaxHeadDim) return dc::wide_ws_bytes(s, bf16, false);  // required, not optional
     size_t n = fwd_order_ws(s);
     if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s) + round_up(dc::fwd_bf16_split_bytes(s));
     else n += round_up(dc::fwd_f32_split_bytes(s));
@@ -165,6 +164,11 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     };
     l.dsum = take((size_t)s.B * s.H * s.L * sizeof(float));
     l.part = at;
+    if (s.E > dc::kFlashMaxHeadDim) {  // head dims above 128: the materialized path's buffers
+        take(dc::wide_ws_bytes(s, bf16, true));
+        l.total = at;
+        return l;
+    }
     if (!bf16) take(dc::bwd_f32_part_bytes(s));
     if (bf16) {
         const size_t nq = (size_t)s.B * s.H * s.L * s.E, nk = (size_t)s.B * s.Hkv * s.S * s.E;
@@ -188,7 +192,8 @@ size_t bwd_ws(const dc::AttnShape &s, bool bf16) { return bwd_layout(s, bf16).to
 // copies are used only when they fit.
 size_t bwd_ws_min(const dc::AttnShape &s) { return bwd_layout(s, false).part; }
 
-size_t decode_ws(const dc::AttnShape &s) {
+size_t decode_ws(const dc::AttnShape &s, bool bf16) {
+    if (s.E > dc::kDecodeMaxHeadDim) return dc::wide_ws_bytes(s, bf16, false);
     int split_len = 0;
     const int splits = dc::decode_splits(s, &split_len);
     return round_up((size_t)s.B * s.H * splits * (s.E + 2) * sizeof(float));
@@ -283,6 +288,14 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
+    if (s.E > dc::kFlashMaxHeadDim) {  // materialized over row blocks in the workspace (wide.hip)
+        const bool bf16 = d->dtype == DC_BF16;
+        if (workspace == nullptr || dc::wide_rows(s, bf16, false, workspace_bytes) <= 0)
+            return fail(DC_INVALID_ARGUMENT,
+                        "flash attention forward with head_dim above 128 needs a workspace of "
+                        "dc_sdpa_fwd_workspace_size bytes (at least one row of scores per kv head)");
+        return launched(dc::launch_wide_fwd(a, bf16, workspace, workspace_bytes, static_cast<hipStream_t>(stream)));
+    }
     // A workspace too small (or none) only gives up the longest-first order of key-padding masks,
     // the split key ranges of small grids, and for bf16 the fp16 P V product (the bf16 hi + lo
     // pair is used instead).
@@ -345,7 +358,7 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
     a.dsum = reinterpret_cast<float *>(ws);
     a.dq_acc = bf16 ? nullptr : static_cast<float *>(dq);
     const BwdLayout l = bwd_layout(s, bf16);
-    if (!bf16 && workspace_bytes > l.part) {
+    if (!bf16 && s.E <= dc::kFlashMaxHeadDim && workspace_bytes > l.part) {
         a.dq_part = reinterpret_cast<float *>(ws + l.part);
         a.part_bytes = workspace_bytes - l.part;
     }
@@ -360,6 +373,13 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
         }
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
+    if (s.E > dc::kFlashMaxHeadDim) {  // materialized over row blocks after dsum (wide.hip)
+        if (dc::wide_rows(s, bf16, true, workspace_bytes - l.part) <= 0)
+            return fail(DC_INVALID_ARGUMENT,
+                        "flash attention backward with head_dim above 128 needs a workspace of "
+                        "dc_sdpa_bwd_workspace_size bytes (at least one row of scores per kv head)");
+        return launched(dc::launch_wide_bwd(a, bf16, ws + l.part, workspace_bytes - l.part, strm));
+    }
     if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
     return launched(dc::launch_bwd_bf16(a, strm));
 }
@@ -386,6 +406,7 @@ dc_status dry_run(dc_sdpa_schedule *out, F call) {
     out->split_chunk_q = sch.split_chunk_q;
     out->f16_products = sch.f16_products;
     out->deterministic = sch.deterministic;
+    out->materialized_rows = sch.materialized_rows;
     out->workgroups = sch.workgroups;
     return ok();
 }
@@ -415,7 +436,7 @@ dc_status dc_sdpa_bwd_schedule(const dc_attn_desc *d, int has_mask, size_t works
 size_t dc_sdpa_decode_workspace_size(const dc_attn_desc *d) {
     dc::AttnShape s;
     if (check_dims(d, &s) != DC_OK) return 0;
-    return decode_ws(s);
+    return decode_ws(s, d->dtype == DC_BF16);
 }
 
 dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, const void *v,
@@ -428,7 +449,7 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
     if (s.causal)
         return fail(DC_INVALID_ARGUMENT,
                     "flash attention decode is non-causal (top-left causal at L = 1 sees one key)");
-    if (workspace_bytes < decode_ws(s))
+    if (workspace_bytes < decode_ws(s, d->dtype == DC_BF16))
         return fail(DC_INVALID_ARGUMENT, "flash attention decode workspace is too small");
     const int64_t nq = (int64_t)s.B * s.H, nkv = (int64_t)s.B * s.Hkv * s.S * s.E;
     if (nq == 0) return ok();
@@ -436,6 +457,11 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
         !present(out, nq * s.E) || !present(lse, nq) || !present(workspace, 1))
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    if (s.E > dc::kDecodeMaxHeadDim) {  // the forward's materialized path at L = 1 (wide.hip)
+        dc::FwdArgs f{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
+        return launched(dc::launch_wide_fwd(f, d->dtype == DC_BF16, workspace, workspace_bytes,
+                                            static_cast<hipStream_t>(stream)));
+    }
     dc::DecodeArgs a{};
     a.s = s;
     a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
@@ -453,7 +479,10 @@ dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const voi
     if (s.causal)
         return fail(DC_INVALID_ARGUMENT,
                     "flash attention decode is non-causal (top-left causal at L = 1 sees one key)");
-    const size_t need = decode_ws(s);
+    if (s.E > dc::kDecodeMaxHeadDim)
+        return fail(DC_UNSUPPORTED, "flash attention decode without a workspace takes head_dim up to 256; "
+                                    "use dc_sdpa_decode with a workspace");
+    const size_t need = decode_ws(s, d->dtype == DC_BF16);
     if (need > dc::kDecodeScratchBytes)
         return fail(DC_UNSUPPORTED, "flash attention decode needs " + std::to_string(need) +
                                         " bytes of split partials, more than the " +
@@ -492,6 +521,7 @@ dc_status dc_bmm(const dc_bmm_desc *d, const float *a, const float *b, float *c,
     g.batch = (int)d->batch, g.m = (int)d->m, g.n = (int)d->n, g.k = (int)d->k;
     g.sab = d->a_stride_batch, g.sam = d->a_stride_m, g.sak = d->a_stride_k;
     g.sbb = d->b_stride_batch, g.sbk = d->b_stride_k, g.sbn = d->b_stride_n;
+    g.scb = d->m * d->n, g.scm = d->n, g.acc = false;
     return launched(dc::launch_bmm(g, static_cast<hipStream_t>(stream)));
 }
 

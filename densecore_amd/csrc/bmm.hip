@@ -14,7 +14,9 @@
 // are; 16-byte loads along k are stored transposed (lanes along m or n, conflict-free); other
 // layouts load one element per lane.  The next k tile is loaded into registers while the current
 // one is multiplied (one barrier per k tile).  Accumulation is float32 (the reference sums the
-// products in k order; here the MFMA's order, within the float32 tolerance).
+// products in k order; here the MFMA's order, within the float32 tolerance).  The launcher also
+// serves the attention path of head dims above 128 (wide.hip), which writes C through strides
+// and can add A B into C.
 #include "common.hpp"
 #include "params.hpp"
 
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         __syncthreads();
     }
 
-    float *cp = g.c + (int64_t)bt * g.m * g.n;
+    float *cp = g.c + (int64_t)bt * g.scb;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -164,7 +166,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm * (BM / 2) + 32 * i + acc_row(e, gh);
-                if (row < g.m && col < g.n) cp[(int64_t)row * g.n + col] = acc[i][j][e];
+                if (row < g.m && col < g.n) {
+                    float *dst = cp + (int64_t)row * g.scm + col;
+                    *dst = g.acc ? *dst + acc[i][j][e] : acc[i][j][e];
+                }
             }
         }
 }
@@ -203,10 +208,13 @@ hipError_t launch_t(const BmmArgs &g, hipStream_t st) {
     return launch_b<BM, BN, SCALAR>(g, lb, grid, st);
 }
 
-// Zeroes C when k == 0 (the reference returns zeros).
-__global__ __launch_bounds__(256) void bmm_zero_kernel(float *c, int64_t count) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256)
-        c[i] = 0.f;
+// Zeroes C when k == 0 (the reference returns zeros); C is (batch, m, n) through its strides.
+__global__ __launch_bounds__(256) void bmm_zero_kernel(BmmArgs g) {
+    const int64_t count = (int64_t)g.batch * g.m * g.n;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+        const int64_t bt = i / ((int64_t)g.m * g.n), r = i % ((int64_t)g.m * g.n);
+        g.c[bt * g.scb + (r / g.n) * g.scm + r % g.n] = 0.f;
+    }
 }
 
 }  // namespace
@@ -214,9 +222,10 @@ __global__ __launch_bounds__(256) void bmm_zero_kernel(float *c, int64_t count) 
 hipError_t launch_bmm(const BmmArgs &g, hipStream_t st) {
     if (g.batch == 0 || g.m == 0 || g.n == 0) return hipSuccess;
     if (g.k == 0) {
+        if (g.acc) return hipSuccess;
         const int64_t count = (int64_t)g.batch * g.m * g.n;
         const int64_t blocks = (count + 255) / 256 < 65536 ? (count + 255) / 256 : 65536;
-        return launch(bmm_zero_kernel, dim3((unsigned)blocks), dim3(256), st, g.c, count);
+        return launch(bmm_zero_kernel, dim3((unsigned)blocks), dim3(256), st, g);
     }
     // 128 x 64 tiles when n is narrow (the weights-times-v product of attention, n = head dim).
     if (g.n <= 64) return launch_t<128, 64>(g, st);

@@ -186,6 +186,7 @@ struct Schedule {
     int split_chunk_k = 0, split_chunk_q = 0;  // bf16 backward split grids
     int f16_products = 0;                   // bf16 products on the fp16 copies
     int deterministic = 1;                  // backward results identical from run to run
+    int materialized_rows = 0;              // head dims above 128: rows per block (wide.hip)
     int64_t workgroups = 0;                 // workgroups of the launches, summed
 };
 inline thread_local Schedule *g_schedule = nullptr;

@@ -216,7 +216,8 @@ template <typename T>
 hipError_t launch_dtype(const DecodeArgs &a, hipStream_t st) {
     if (a.s.E <= 32) return launch_t<T, 32>(a, st);
     if (a.s.E <= 64) return launch_t<T, 64>(a, st);
-    return launch_t<T, 128>(a, st);
+    if (a.s.E <= 128) return launch_t<T, 128>(a, st);
+    return launch_t<T, 256>(a, st);
 }
 
 }  // namespace

@@ -104,8 +104,19 @@ struct BmmArgs {
     int batch, m, n, k;
     int64_t sab, sam, sak;  // A's strides: batch, m, k
     int64_t sbb, sbk, sbn;  // B's strides: batch, k, n
+    int64_t scb, scm;       // C's strides: batch, m (unit stride along n)
+    bool acc;               // C += A B (else C = A B)
 };
 hipError_t launch_bmm(const BmmArgs &g, hipStream_t st);
+
+// Attention for head dims above 128 (wide.hip), materialized over blocks of query rows in the
+// workspace: its full size, the rows per block a given workspace allows (0: too small), and the
+// launchers (the backward's workspace starts after dsum).
+size_t wide_ws_bytes(const AttnShape &s, bool bf16, bool backward);
+int64_t wide_rows(const AttnShape &s, bool bf16, bool backward, size_t bytes);
+hipError_t launch_wide_fwd(const FwdArgs &a, bool bf16, void *ws, size_t bytes, hipStream_t st);
+hipError_t launch_wide_bwd(const BwdArgs &a, bool bf16, void *ws, size_t bytes, hipStream_t st);
+constexpr int kFlashMaxHeadDim = 128;  // the flash kernels' widest instantiation
 
 // Compute units of the current device, and workgroups of `kernel` (`threads` per workgroup) that
 // fit on one of them; both looked up once per device (and kernel) and cached.  0 if unknown.
@@ -138,6 +149,7 @@ int decode_splits(const AttnShape &s, int *split_len);
 // The allocation-free decode's scratch (a static device array in decode.hip): its size, and its
 // address on the current device (looked up with hipGetSymbolAddress once per device).
 constexpr size_t kDecodeScratchBytes = (size_t)16 << 20;
+constexpr int kDecodeMaxHeadDim = 256;  // the split kernel's widest instantiation
 hipError_t decode_scratch(float **ptr);
 // `vec`: rows (and mask rows) start 16-byte aligned and the width is a multiple of 4.
 hipError_t launch_softmax_fwd(const SoftmaxArgs &a, bool vec, hipStream_t st);
@@ -173,7 +185,5 @@ hipError_t launch_dropout_apply(const uint32_t *bits, int64_t n, float scale, co
                                 float *y, hipStream_t st);
 }  // namespace mt
 
-// Largest head dim each kernel family instantiates.
-constexpr int kMaxHeadDim = 256;
 
 }  // namespace dc

@@ -48,7 +48,7 @@ extern "C" {
 typedef enum {
     DC_OK = 0,
     DC_INVALID_ARGUMENT = 1, /* shape / argument errors: the reference raises ValueError */
-    DC_UNSUPPORTED = 2,      /* outside what the kernels implement (e.g. E > 128) */
+    DC_UNSUPPORTED = 2,      /* outside what the kernels implement (e.g. dims >= 2^31) */
     DC_EXECUTION_FAILED = 3  /* a HIP launch or runtime error: the reference's RuntimeError */
 } dc_status;
 
@@ -67,8 +67,10 @@ typedef struct {
 /* Version of this ABI (bumped on any incompatible change). */
 int dc_abi_version(void);
 
-/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  The workspace is
- * optional: it holds the longest-first workgroup order of a query-independent mask
+/* Forward (out, lse).  src/lib.rs:609-638, src/torch_attention.rs:143-284.  Any head_dim: up to
+ * 128 the flash kernels, above 128 the same mathematics materialized over blocks of query rows in
+ * the workspace (required then; a smaller one than the size returned only shortens the blocks).
+ * Up to 128 the workspace is optional: it holds the longest-first workgroup order of a query-independent mask
  * (mask_stride_l == 0, e.g. key padding); for float32 without a mask, when the query tiles fill
  * at most half of the current device, the partial outputs of split key ranges (so the size
  * depends on the device current at the call); for bf16 without a mask, the power-of-two-scaled
@@ -96,7 +98,8 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
                       void *stream);
 
 /* Single-query (q_len == 1), non-causal attention over a contiguous KV cache, split over the
- * keys and merged.  Same results as dc_sdpa_fwd at q_len == 1 (the reference's decode). */
+ * keys and merged (head_dim up to 256; above, the forward's materialized path at L = 1).  Same
+ * results as dc_sdpa_fwd at q_len == 1 (the reference's decode). */
 size_t dc_sdpa_decode_workspace_size(const dc_attn_desc *d);
 dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, const void *v,
                          void *out, float *lse, void *workspace, size_t workspace_bytes,
@@ -129,7 +132,7 @@ typedef struct {
     int32_t split_chunk_q;  /* bf16 backward: key tiles per dQ piece; 0: whole query tiles */
     int32_t f16_products;   /* bf16: 1 when the products run on the scaled fp16 copies */
     int32_t deterministic;  /* backward: 1 when dq, dk, dv are identical from run to run */
-    int32_t reserved;
+    int32_t materialized_rows; /* head_dim > 128: query rows per materialized block; 0: flash */
     int64_t workgroups;     /* workgroups of all the call's launches */
 } dc_sdpa_schedule;
 

@@ -115,7 +115,6 @@ def fwd(d, mask=None):
     (dict(kv_heads=0), _lib.DC_INVALID_ARGUMENT, "q/k/v shapes do not match"),
     (dict(q_len=-1), _lib.DC_INVALID_ARGUMENT, r"takes \(B, H, L, E\) tensors"),
     (dict(dtype=7), _lib.DC_INVALID_ARGUMENT, "dtype"),
-    (dict(head_dim=300), _lib.DC_UNSUPPORTED, "head_dim"),
     (dict(q_len=2**31), _lib.DC_UNSUPPORTED, "2\\^31"),
 ])
 def test_forward_argument_errors(kw, status, msg):
@@ -237,3 +236,24 @@ def test_bmm_descriptor_layout_matches_header(tmp_path):
                                        check=True).stdout.split()))
     D = _lib.BmmDesc
     assert got == [ctypes.sizeof(D), D.a_stride_batch.offset, D.b_stride_n.offset]
+
+
+def test_wide_head_dims_take_the_materialized_path():
+    """Head dims above 128 run materialized over row blocks in the workspace (any head dim, as
+    the reference's kernels take any): the schedule query reports the rows per block, the
+    workspace is required, and a smaller one only shortens the blocks."""
+    L = _lib.lib()
+    out = _lib.Schedule()
+    for dtype in (_lib.DC_F32, _lib.DC_BF16):
+        d = desc(head_dim=300, dtype=dtype, q_len=50, kv_len=70)
+        full = L.dc_sdpa_fwd_workspace_size(ctypes.byref(d))
+        assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, full, ctypes.byref(out)) == _lib.DC_OK
+        assert out.materialized_rows == 2 * 50  # repeat (4 / 2) x L rows per (batch, kv head)
+        assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, 0, ctypes.byref(out)) == _lib.DC_INVALID_ARGUMENT
+        assert b"head_dim above 128 needs a workspace" in L.dc_last_error()
+        one_row = full - (2 * 50 - 1) * 2 * 2 * 70 * 4  # full minus 99 rows of (items x S) floats
+        assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, one_row, ctypes.byref(out)) == _lib.DC_OK
+        assert 1 <= out.materialized_rows < 2 * 50
+        bw = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
+        assert L.dc_sdpa_bwd_schedule(ctypes.byref(d), 0, bw, ctypes.byref(out)) == _lib.DC_OK
+        assert out.materialized_rows == 2 * 50 and out.deterministic == 1
