@@ -499,7 +499,7 @@ def main():
         line["ms_per_step"] = round(c2["ms_per_step"], 4)
         line["roofline"] = roofline(
             c2["bwd_tflops"], PEAK_FP32_MFMA, "TFLOP/s", "mfma", traffic.get("C2_bwd"),
-            "dc_sdpa_bwd (bwd_pre_kernel + bwd_f32_kernel)",
+            "dc_sdpa_bwd (bwd_pre_f32_kernel + bwd_f32_kernel + bwd_reduce_f32_kernel)",
             f"{c2['bwd_flop'] / 1e9:.3f} GFLOP per call / {c2['bwd_ms']:.4f} ms (HIP events around "
             f"{c2['timing_calls']} back-to-back calls)")
         line["forward_roofline"] = roofline(

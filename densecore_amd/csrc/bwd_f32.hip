@@ -234,23 +234,32 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     const float *vb = static_cast<const float *>(a.v) + (int64_t)bhk * s.S * s.E;
 
     // K and V rows of this lane's key: K[key][g*DH + t], V[key][g*DH + t].
-    float kreg[DH], vreg[DH];
+    // At D = 128 the K row is not held in registers: S reads it from the workgroup's transposed
+    // K tile in LDS (which the dQ product needs anyway), one ds_read_b32 of 32 consecutive keys
+    // per half-wave and MFMA.  K and V rows plus the dK / dV accumulators (4 x 64 floats per lane)
+    // would not fit one wave's registers without spills.
+    constexpr bool KREG = D <= 64;
+    float kreg[KREG ? DH : 1], vreg[DH];
     {
         const float *kr = kb + (int64_t)key * s.E, *vr = vb + (int64_t)key * s.E;
         if (VEC && key < s.S) {
 #pragma unroll
             for (int t = 0; t < DH; t += 4) {
-                const f32x4 x = *reinterpret_cast<const f32x4 *>(kr + g * DH + t);
                 const f32x4 y = *reinterpret_cast<const f32x4 *>(vr + g * DH + t);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) kreg[t + u] = x[u], vreg[t + u] = y[u];
+                for (int u = 0; u < 4; ++u) vreg[t + u] = y[u];
+                if constexpr (KREG) {
+                    const f32x4 x = *reinterpret_cast<const f32x4 *>(kr + g * DH + t);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) kreg[t + u] = x[u];
+                }
             }
         } else {
 #pragma unroll
             for (int t = 0; t < DH; ++t) {
                 const int d = g * DH + t;
                 const bool ok = key < s.S && d < s.E;
-                kreg[t] = ok ? kr[d] : 0.f;
+                if constexpr (KREG) kreg[t] = ok ? kr[d] : 0.f;
                 vreg[t] = ok ? vr[d] : 0.f;
             }
         }
@@ -341,7 +350,8 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
             const f32x4 oo = *reinterpret_cast<const f32x4 *>(&sm.dout[lr][g * DH + t4]);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                sacc = mfma_f32(qq[u], kreg[t4 + u], sacc);
+                const float kk = KREG ? kreg[KREG ? t4 + u : 0] : sm.kt[g * DH + t4 + u][wave * 32 + lr];
+                sacc = mfma_f32(qq[u], kk, sacc);
                 pacc = mfma_f32(oo[u], vreg[t4 + u], pacc);
             }
             if (t4 % 8 == 4) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
@@ -534,9 +544,9 @@ __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(BwdArgs a, StreamK sk,
 
 // The reductions of the deterministic float32 backward.  Blocks below dq_blocks: dq = scale *
 // the sum of the key tiles' dQ slots in tile order, one thread per 4 dims of a row.  With a
-// stream-K schedule, each further block finishes one key tile: a cut tile's dK / dV are the sum
-// of its ranges' slots in range order; a tile without steps gets zeros; the others were stored
-// by their one workgroup.
+// stream-K schedule, the further blocks finish the key tiles, several blocks per tile and 4 floats
+// per thread: a cut tile's dK / dV are the sum of its ranges' slots in range order; a tile without
+// steps gets zeros; the others were stored by their one workgroup.
 // vec4: E % 4 == 0 and dq 16-byte aligned (16-byte loads and stores).
 __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK sk, int dq_blocks, bool vec4) {
     const AttnShape &s = a.s;
@@ -575,26 +585,43 @@ __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK 
         }
         return;
     }
-    const int t = blockIdx.x - dq_blocks, bhk = t / nkt, kt = t % nkt;
+    // kv_blocks blocks per key tile, one 16-byte chunk (4 floats) of dK and of dV per thread.
+    const int kv_blocks = (kBN * s.E / 4 + 255) / 256;
+    const int u = blockIdx.x - dq_blocks, t = u / kv_blocks, part = u % kv_blocks;
+    const int bhk = t / nkt, kt = t % nkt;
     const SkTile tile = sk_tile(s, sk, bhk, kt);
     if (tile.n > 0 && !tile.cut) return;  // stored by its one workgroup
     const int n0 = kt * kBN, n1 = min(s.S, n0 + kBN);
-    const int64_t base = ((int64_t)bhk * s.S + n0) * s.E, count = (int64_t)(n1 - n0) * s.E;
-    float *dk = static_cast<float *>(a.dk) + base, *dv = static_cast<float *>(a.dv) + base;
+    const int64_t count = (int64_t)(n1 - n0) * s.E;
+    const int64_t j = ((int64_t)part * 256 + threadIdx.x) * 4;
+    if (j >= count) return;
+    const int64_t base = ((int64_t)bhk * s.S + n0) * s.E;
+    float *dk = static_cast<float *>(a.dk) + base + j, *dv = static_cast<float *>(a.dv) + base + j;
     const int64_t c0 = tile.n > 0 ? chunk_of(sk, tile.ts) : 0, c1 = tile.n > 0 ? chunk_of(sk, tile.ts + tile.n - 1) : -1;
     // Range c0 starts inside this tile (slot 0) unless it began in an earlier tile (slot 1); the
     // later ranges all start inside it.  With more ranges than steps some ranges are empty: they
     // wrote nothing and are skipped.
     const bool c0_starts_here = c0 * sk.total / sk.chunks >= tile.ts;
-    for (int64_t j = threadIdx.x; j < count; j += 256) {
-        float sk_ = 0.f, sv = 0.f;
-        for (int64_t c = c0; c <= c1; ++c) {
-            if ((c + 1) * sk.total / sk.chunks == c * sk.total / sk.chunks) continue;  // empty range
-            const float *slot = kv_slot(a, c, (c == c0 && !c0_starts_here) ? 1 : 0);
-            sk_ += slot[j];
-            sv += slot[(int64_t)kBN * s.E + j];
+    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, av = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t c = c0; c <= c1; ++c) {
+        if ((c + 1) * sk.total / sk.chunks == c * sk.total / sk.chunks) continue;  // empty range
+        const float *slot = kv_slot(a, c, (c == c0 && !c0_starts_here) ? 1 : 0) + j;
+        if (vec4) {
+            ak += *reinterpret_cast<const f32x4 *>(slot);
+            av += *reinterpret_cast<const f32x4 *>(slot + (int64_t)kBN * s.E);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (j + e < count) ak[e] += slot[e], av[e] += slot[(int64_t)kBN * s.E + e];
         }
-        dk[j] = sk_, dv[j] = sv;
+    }
+    if (vec4) {
+        *reinterpret_cast<f32x4 *>(dk) = ak;
+        *reinterpret_cast<f32x4 *>(dv) = av;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (j + e < count) dk[e] = ak[e], dv[e] = av[e];
     }
 }
 
@@ -680,8 +707,10 @@ hipError_t launch_d(const BwdArgs &args, size_t part_bytes, hipStream_t st) {
     if (!a.dq_part) return hipSuccess;
     const int64_t dq_threads = rows * ((a.s.E + 3) / 4);
     const int dq_blocks = (int)((dq_threads + 255) / 256);
-    const int64_t reduce_blocks = dq_blocks + (sk.chunks > 0 ? tiles : 0);
-    const bool vec4 = args.s.vec && (a.s.E & 3) == 0;  // the ABI's s.vec: every pointer 16-byte aligned
+    const int64_t kv_blocks = (kBN * a.s.E / 4 + 255) / 256;  // per key tile
+    const int64_t reduce_blocks = dq_blocks + (sk.chunks > 0 ? tiles * kv_blocks : 0);
+    // The ABI's s.vec: every pointer (dq, dk, dv included) 16-byte aligned.
+    const bool vec4 = args.s.vec && (a.s.E & 3) == 0;
     return launch(bwd_reduce_f32_kernel, dim3((unsigned)reduce_blocks), dim3(256), st, a, sk, dq_blocks, vec4);
 }
 
