@@ -48,7 +48,9 @@ def _check_device(*tensors):
 
 def _mask_arg(mask, dims, dev):
     """``attention_mask`` (src/lib.rs:594-607): an additive float32 (B, H, L, S) mask.
-    Broadcast views (stride 0) are passed through without materialising them."""
+    Broadcast views (stride 0) are passed through without materialising them.  The kernels read
+    a row's keys with unit stride, so a mask without it (e.g. an (L, 1) mask expanded over the keys)
+    is copied along the key axis only: its broadcast batch / head / query dims stay stride 0."""
     if mask is None:
         return None, (0, 0, 0)
     B, H, _, L, S, _ = dims
@@ -57,7 +59,8 @@ def _mask_arg(mask, dims, dev):
     if mask.device != dev or mask.dtype != torch.float32:
         mask = mask.to(device=dev, dtype=torch.float32)
     if S > 1 and mask.stride(3) != 1:
-        mask = mask.contiguous()
+        distinct = tuple(slice(0, 1) if mask.stride(i) == 0 else slice(None) for i in range(3))
+        mask = mask[distinct].contiguous().expand(B, H, L, S)
     return mask, (mask.stride(0), mask.stride(1), mask.stride(2))
 
 

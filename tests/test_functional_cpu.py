@@ -99,3 +99,22 @@ def test_flash_mask_rejections(mask):
     assert F._flash_mask(mask, (2, 4, 3, 8), 5, "cpu") is None
     req = torch.zeros((3, 5), requires_grad=True)
     assert F._flash_mask(req, (2, 4, 3, 8), 5, "cpu") is None
+
+
+@pytest.mark.parametrize("shape", [(3, 1), (1, 1, 3, 1), (2, 1, 3, 1), (1, 4, 1, 1), (2, 4, 3, 1)])
+def test_mask_broadcast_over_keys_copies_the_key_axis_only(shape):
+    """A mask without unit key stride (an (L, 1) mask expanded over S, say) reaches the kernels
+    as a copy along the key axis whose other broadcast dims keep stride 0: never B*H*L*S floats
+    unless the mask really has B*H*L distinct rows."""
+    B, H, L, S = 2, 4, 3, 5
+    rng = np.random.default_rng(1)
+    src = torch.from_numpy(rng.normal(size=shape).astype(np.float32))
+    full = (1,) * (4 - len(shape)) + tuple(shape)  # the mask's own (B|1, H|1, L|1, 1)
+    view = src.reshape(full).expand(B, H, L, S)
+    m, strides = _native._mask_arg(view, (B, H, H, L, S, 8), torch.device("cpu"))
+    assert m.stride(3) == 1 and strides == (m.stride(0), m.stride(1), m.stride(2))
+    np.testing.assert_array_equal(m.numpy(), view.numpy())
+    for dim in range(3):
+        if full[dim] == 1:
+            assert m.stride(dim) == 0, (dim, m.stride())
+    assert m.untyped_storage().nbytes() == 4 * S * int(np.prod([full[d] for d in range(3)]))

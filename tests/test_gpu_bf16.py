@@ -114,16 +114,16 @@ def c5_run():
     return d, res
 
 
-HEADS = [(0, 0), (1, 17)]
+HEADS = [(0, 0), (1, 17), (0, 31), (1, 31)]  # (batch, head): first, middle and last heads
 
 
 @pytest.mark.parametrize("a,b", [(0, 1024), (4096, 4224), (7168, 8192)])
 def test_c5_windows(oracle_lib, c5_run, a, b):
     d, res = c5_run
-    sel = lambda x, rows: np.stack([x[bi, hi, rows] for bi, hi in HEADS])[None]  # (1, 2, n, E)
+    sel = lambda x, rows: np.stack([x[bi, hi, rows] for bi, hi in HEADS])[None]  # (1, len(HEADS), n, E)
     q, g = sel(d["q"], slice(a, b)), sel(d["g"], slice(a, b))
     k, v = sel(d["k"], slice(0, b)), sel(d["v"], slice(0, b))
-    mask = np.ascontiguousarray(np.broadcast_to(_offset_causal(b - a, b, a), (1, 2, b - a, b)))
+    mask = np.ascontiguousarray(np.broadcast_to(_offset_causal(b - a, b, a), (1, len(HEADS), b - a, b)))
     print(f"[case] C5 window rows [{a}, {b})", flush=True)
     ref_o, ref_l = oracle_lib.forward(q, k, v, False, None, mask)
     assert_bf16(sel(res["out"], slice(a, b)), ref_o, f"C5 out[{a}:{b}]")

@@ -139,6 +139,35 @@ def test_row_broadcast_masks(oracle_lib, B, H, L, S, E, kind):
         assert_f32(a.cpu().numpy(), b, f"row-{kind} {name}")
 
 
+@pytest.mark.parametrize("shape", [(1, 1, 70, 1), (2, 1, 70, 1), (2, 3, 70, 1)])
+def test_key_broadcast_masks(oracle_lib, shape):
+    """A mask constant along the keys (an (L, 1)-shaped row bias, stride 0 over S) is copied
+    along the key axis only and keeps its other broadcast strides; rows at -inf are fully
+    masked (out 0, lse 0, zero gradients)."""
+    from densecore_amd import _native
+    B, H, L, S, E = 2, 3, 70, 90, 64
+    rng = np.random.default_rng(sum(shape))
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, H, S, E), dtype=np.float32) for _ in range(2))
+    small = rng.standard_normal(shape).astype(np.float32)
+    small[..., ::7, :] = -np.inf
+    view = _t(small).expand(B, H, L, S)
+    m, _ = _native._mask_arg(view, (B, H, H, L, S, E), view.device)
+    assert m.untyped_storage().nbytes() == small.size * S * 4
+    full = np.ascontiguousarray(np.broadcast_to(small, (B, H, L, S)))
+    print(f"[case] key-broadcast mask {shape}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False, None, full)
+    out, lse = _native._flash_attention(_t(q), _t(k), _t(v), False, None, view)
+    torch.cuda.synchronize()
+    assert_f32(out.cpu().numpy(), ref_o, "key-broadcast out")
+    assert_f32(lse.cpu().numpy(), ref_l, "key-broadcast lse")
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, False, None, full)
+    got = _native._flash_attention_backward(_t(g), _t(q), _t(k), _t(v), _t(ref_o), _t(ref_l), False,
+                                            None, view)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_f32(a.cpu().numpy(), b, f"key-broadcast {name}")
+
+
 @pytest.mark.parametrize("mode", ["none", "causal", "bool", "float"])
 def test_attention_rank4(oracle_lib, mode):
     """tests/test_attention.py:12-39, rank-4 (2, 3, 4, 8) cases."""
