@@ -405,11 +405,14 @@ def cpu_baseline(threads, gpu):
 
 # Shapes whose whole-tile grids fill little of the device (few heads, long rows), where the
 # alternative schedules run: the split forward (float32, bf16), the float32 backward's stream-K
-# ranges and the bf16 backward's split grids.  Not part of the default run (--only sched).
+# ranges and the bf16 backward's split grids; and head dim 256, which runs materialized over row
+# blocks (its FLOPs count the causal half only, as everywhere).  Not part of the default run
+# (--only sched).
 SCHED_SHAPES = [  # B, H, L, E, causal, dtype
     (1, 8, 2048, 64, True, "f32"), (1, 4, 4096, 64, True, "f32"), (1, 8, 2048, 128, True, "f32"),
     (8, 12, 512, 64, True, "f32"), (6, 16, 1024, 64, False, "f32"),
     (1, 1, 16384, 128, True, "bf16"), (1, 2, 8192, 128, True, "bf16"), (1, 4, 4096, 128, True, "bf16"),
+    (2, 16, 2048, 256, True, "f32"), (2, 16, 2048, 256, True, "bf16"),
 ]
 
 

@@ -112,6 +112,10 @@ constexpr float kLoP = 0x1p-4f;
 // P >= kLoP are normal fp16 numbers (>= 2^-2); dV is scaled back at the end (P <= 1, so P times
 // 2^14 stays below fp16's largest value even for an lse a few units off).
 constexpr int kPShift = 14;
+// dS = P (dP - dsum) 2^(e_do + e_v - 24) of the fp16 mode is formed from P 2^kPShift times
+// 2^-kDsShift: the kernel computes p 2^(kPShift - kDsShift) = p 2^-24 directly (the exponent
+// carries it), and P 2^kPShift from that by 2^kDsShift (exact).
+constexpr int kDsShift = kPShift + 24;
 
 template <bool F16>
 DEVI f32x16 mfma16(bf16x8 x, bf16x8 y, f32x16 c) {
@@ -188,14 +192,15 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         fill_cm<kKM, D, VEC, kKW>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, lane);
         fill_cm<kKM, D, VEC, kKW>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, lane);
     };
-    // -lse log2 e (-inf past L: P = 0 there) and dsum of a step, one value per lane of waves
+    // -lse log2 e (-inf past L: P = 0 there) and -dsum of a step, one value per lane of waves
     // 0 and 1.  (The float32 kernels subtract lse in natural-log units first, which saves one
     // rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
     auto load_row_stat = [&](int i) -> float {
         const int bh = step_bh(i), qq = step_m0(i) + lane;
         if (wave == 0)
-            return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e + (F16 ? (float)kPShift : 0.f) : -INFINITY;
-        const float ds = qq < s.L ? a.dsum[(int64_t)bh * s.L + qq] : 0.f;
+            return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e + (F16 ? (float)(kPShift - kDsShift) : 0.f)
+                            : -INFINITY;
+        const float ds = qq < s.L ? -a.dsum[(int64_t)bh * s.L + qq] : 0.f;
         return F16 ? ldexpf(ds, fs.e_pv) : ds;
     };
     auto store_row_stat = [&](int i, float x) {
@@ -232,9 +237,20 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
         const bool live = kw0 < s.S && mq < s.L && (!CAUSAL || mq + 31 >= kw0);
         if (live) {
+            // dP accumulates onto -dsum, so the MFMAs leave dP - dsum.  The rows' -lse log2 e are
+            // read here too: LDS reads complete in order, and read after the first product
+            // group's operands they would make the elementwise work wait for those.
             f32x16 sacc, pacc;
+            f32x4 nl[4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int row0 = 32 * qh + 8 * r4 + 4 * g;  // rows of registers 4 r4 .. 4 r4 + 3
+                const f32x4 nd = *reinterpret_cast<const f32x4 *>(&sm.m.dsum[buf][row0]);
+                nl[r4] = *reinterpret_cast<const f32x4 *>(&sm.m.lse[buf][row0]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sacc[4 * r4 + j] = 0.f, pacc[4 * r4 + j] = nd[j];
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep these reads out of the MFMA schedule below
 #pragma unroll
             for (int st = 0; st < KSTEP; ++st) {
                 sacc = mfma16<F16>(row_frag<kKM, D>(qt, rowb, 32 * qh, st),
@@ -244,15 +260,30 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
             }
             // Keep the operand reads (two per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 2, 4>();
-            // P and dS; EDGE (keys past S or crossing the diagonal) is a separate
-            // instantiation so that the common path carries no per-element masking.
+            __builtin_amdgcn_sched_barrier(0);
+
+            // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA, in four groups: (16-query
+            // half u = 0, P), (0, dS), (1, P), (1, dS).  A group's transposed operand (dO^T or
+            // Q^T) is read while the previous group's MFMAs run; the first one's while P and dS
+            // are formed.
+            bf16x8 fa[2][NDT];
+            auto load_group = [&](int grp, bf16x8 *dst) {
+                const u32x4 *t = (grp & 1) ? qt : ot;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) dst[dt] = tr_frag<kKM, D>(t, trb, 32 * qh + 16 * (grp >> 1), dt);
+            };
+            load_group(0, fa[0]);
+
+            // P and dS.  F16: sacc becomes p 2^-24 (the exponent carries kPShift - kDsShift), so
+            // that dS = sacc (dP - dsum) needs one multiply, and P 2^kPShift = sacc 2^kDsShift;
+            // both are rounded to fp16 in the product groups.  Otherwise sacc = p and pacc = dS.
+            // EDGE (keys past S or crossing the diagonal) is a separate instantiation so that the
+            // common path carries no per-element masking.
             auto elementwise = [&](auto edge_c) {
                 constexpr bool EDGE = decltype(edge_c)::value;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
-                    const int row0 = 32 * qh + 8 * r4 + 4 * g;  // rows of registers 4 r4 .. 4 r4 + 3
-                    const f32x4 nl = *reinterpret_cast<const f32x4 *>(&sm.m.lse[buf][row0]);
-                    const f32x4 dsm = *reinterpret_cast<const f32x4 *>(&sm.m.dsum[buf][row0]);
+                    const int row0 = 32 * qh + 8 * r4 + 4 * g;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int r = 4 * r4 + j, qq = m0 + row0 + j;
@@ -260,52 +291,47 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                         float x;
                         if (MASK) {
                             const float mk = (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-                            x = fmaf(fmaf(sacc[r], sc, mk), kLog2e, nl[j]);
+                            x = fmaf(fmaf(sacc[r], sc, mk), kLog2e, nl[r4][j]);
                         } else {
-                            x = fmaf(sacc[r], sc_log2, nl[j]);
+                            x = fmaf(sacc[r], sc_log2, nl[r4][j]);
                         }
                         if (EDGE && (key >= s.S || (CAUSAL && key > qq))) x = -INFINITY;
                         const float p = exp2_fast(x);
                         sacc[r] = p;
-                        pacc[r] = F16 ? p * (pacc[r] - dsm[j]) * 0x1p-38f : p * (pacc[r] - dsm[j]);
+                        if constexpr (!F16) pacc[r] = p * pacc[r];
                     }
                 }
             };
             if (kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > mq)) elementwise(std::true_type{});
             else elementwise(std::false_type{});
 
-            // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA.
+            bool lo = false;  // F16: this half's P and dS also enter as their rounding errors
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int row0 = 32 * qh + 16 * u;
+            for (int grp = 0; grp < 4; ++grp) {
+                const int u = grp >> 1;
+                if (grp + 1 < 4) load_group(grp + 1, fa[(grp + 1) & 1]);
+                const bf16x8 *f = fa[grp & 1];
+                f32x16 *acc = (grp & 1) ? dk : dv;
                 bf16x8 ph, pl;
-                bool lo = false;  // F16: this block's P and dS also enter as their rounding errors
                 if constexpr (F16) {
-                    ph = cvt_f16x8(sacc, 8 * u);
-                    lo = any_above(sacc, 8 * u, kLoP * (float)(1 << kPShift));
+                    if (grp & 1) {
+                        ph = cvt_f16x8_prod(sacc, pacc, 8 * u);
+                    } else {
+                        ph = cvt_f16x8_mul(sacc, 8 * u, 0x1p+38f);
+                        lo = any_above_nonneg(sacc, 8 * u, kLoP * 0x1p-24f);
+                    }
                 } else {
-                    split_bf16(sacc, 8 * u, ph, pl);
+                    split_bf16((grp & 1) ? pacc : sacc, 8 * u, ph, pl);
                 }
-                bf16x8 fa[NDT];
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(ot, trb, row0, dt);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma16<F16>(fa[dt], ph, dv[dt]);
+                for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma16<F16>(f[dt], ph, acc[dt]);
                 if (!F16 || lo) {
-                    if constexpr (F16) pl = cvt_f16x8_lo(sacc, 8 * u, ph);
+                    if constexpr (F16) {
+                        pl = (grp & 1) ? cvt_f16x8_prod_lo(sacc, pacc, 8 * u, ph)
+                                       : cvt_f16x8_mul_lo(sacc, 8 * u, 0x1p+38f, ph);
+                    }
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dv[dt] = mfma16<F16>(fa[dt], pl, dv[dt]);
-                }
-                if constexpr (F16) ph = cvt_f16x8(pacc, 8 * u);
-                else split_bf16(pacc, 8 * u, ph, pl);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kKM, D>(qt, trb, row0, dt);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma16<F16>(fa[dt], ph, dk[dt]);
-                if (!F16 || lo) {
-                    if constexpr (F16) pl = cvt_f16x8_lo(pacc, 8 * u, ph);
-#pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dk[dt] = mfma16<F16>(fa[dt], pl, dk[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma16<F16>(f[dt], pl, acc[dt]);
                 }
             }
         }
@@ -454,7 +480,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const float lse_q = qi < s.L ? a.lse[(int64_t)bh * s.L + qi] : 0.f;
     // -lse in base 2.  (The float32 kernels subtract lse in natural-log units first, which
     // saves one rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
-    const float nlse2 = -lse_q * kLog2e;
+    // F16: the exponent also carries the 2^-24 of dS = P (dP - dsum) 2^(e_do + e_v - 24), so
+    // sacc = 2^x (dP - dsum) needs no further scaling.
+    const float nlse2 = -lse_q * kLog2e - (F16 ? 24.f : 0.f);
     float dsum_q = qi < s.L ? a.dsum[(int64_t)bh * s.L + qi] : 0.f;
     if constexpr (F16) dsum_q = ldexpf(dsum_q, fs.e_pv);
     const float *mrow = nullptr;
@@ -510,6 +538,12 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt) {
             if (!live[kt]) continue;
+            // Issue priority: a wave raises it for its MFMA stretches and drops it for the
+            // elementwise work, so that of the waves sharing a SIMD (two workgroups per CU) the
+            // one with MFMAs to issue goes first and the other's VALU work fills in around them
+            // (C5: 1646 -> 1530 us with the K^T reads ahead; the dK/dV kernel, whose two waves
+            // per SIMD pass the same barriers, measured no difference).
+            __builtin_amdgcn_s_setprio(1);
             f32x16 sacc, pacc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
@@ -520,10 +554,22 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
             }
             // Keep the operand reads (one per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 1, 4>();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            // K^T for dQ^T += K^T dS^T, one 16-key half u at a time.  Without a mask both halves
+            // are read here, while dS^T is formed; the masked kernels (whose mask values take 32
+            // more registers) read each just before its products.
+            bf16x8 fa[2][NDT];
+            auto load_fa = [&](int u) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) fa[u][dt] = tr_frag<kQN, D>(kt_, trb, 32 * kt + 16 * u, dt);
+            };
+            if constexpr (!MASK) load_fa(0), load_fa(1);
             // dS^T; EDGE (keys past S or past the diagonal) is a separate instantiation so
-            // that the common path carries no per-element masking.  big[u]: some P of the
-            // 16-key half u exceeds kLoP (its dS then also enters as its rounding error).
-            bool big[2] = {false, false};
+            // that the common path carries no per-element masking.  pm[u]: the largest P 2^-24
+            // of the 16-key half u, as bits (P >= 0 orders as an unsigned integer); where some P
+            // exceeds kLoP, dS also enters as its rounding error.
+            uint32_t pm[2] = {0u, 0u};
             auto elementwise = [&](auto edge_c) {
                 constexpr bool EDGE = decltype(edge_c)::value;
 #pragma unroll
@@ -536,33 +582,32 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                         const int key = n0 + kt * 32 + acc_row(r, g);
                         if (key >= s.S || (CAUSAL && key > qi)) x = -INFINITY;
                     }
-                    if (F16) big[r >> 3] |= x > -4.f;  // P = 2^x > kLoP = 2^-4
-                    sacc[r] = F16 ? exp2_fast(x) * (pacc[r] - dsum_q) * 0x1p-24f
-                                  : exp2_fast(x) * (pacc[r] - dsum_q);
+                    const float p = exp2_fast(x);
+                    if (F16) pm[r >> 3] = max(pm[r >> 3], __float_as_uint(p));
+                    sacc[r] = p * (pacc[r] - dsum_q);
                 }
             };
             if (edge) elementwise(std::true_type{});
             else elementwise(std::false_type{});
             // dQ^T += K^T dS^T, 16 keys per MFMA.
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 bf16x8 sh, sl;
                 bool lo = false;  // F16: this block's dS also enters as its rounding error
                 if constexpr (F16) {
                     sh = cvt_f16x8(sacc, 8 * u);
-                    lo = __builtin_amdgcn_ballot_w64(big[u]) != 0;
+                    lo = __builtin_amdgcn_ballot_w64(pm[u] > __float_as_uint(kLoP * 0x1p-24f)) != 0;
                 } else {
                     split_bf16(sacc, 8 * u, sh, sl);
                 }
-                bf16x8 fa[NDT];
+                if constexpr (MASK) load_fa(u);
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) fa[dt] = tr_frag<kQN, D>(kt_, trb, 32 * kt + 16 * u, dt);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[dt], sh, dq[dt]);
+                for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[u][dt], sh, dq[dt]);
                 if (!F16 || lo) {
                     if constexpr (F16) sl = cvt_f16x8_lo(sacc, 8 * u, sh);
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[dt], sl, dq[dt]);
+                    for (int dt = 0; dt < NDT; ++dt) dq[dt] = mfma16<F16>(fa[u][dt], sl, dq[dt]);
                 }
             }
         }

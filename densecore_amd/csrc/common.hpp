@@ -64,6 +64,46 @@ DEVI bool any_above(const f32x16 &x, int at, float t) {
     for (int j = 1; j < 8; ++j) m = fmaxf(m, x[at + j]);
     return __builtin_amdgcn_ballot_w64(m > t) != 0;
 }
+// The same for values known to be +0 or positive (t too): their bit patterns order as unsigned
+// integers, so the maximum takes integer max3 operations and no NaN canonicalization.  (The
+// elements are read as values: __builtin_bit_cast of an ext-vector element reads element 0 with
+// this compiler.)
+DEVI bool any_above_nonneg(const f32x16 &x, int at, float t) {
+    uint32_t m = __float_as_uint(x[at]);
+#pragma unroll
+    for (int j = 1; j < 8; ++j) m = max(m, __float_as_uint(x[at + j]));
+    return __builtin_amdgcn_ballot_w64(m > __float_as_uint(t)) != 0;
+}
+
+// fp16 of x[at + j] * m and of x[at + j] * y[at + j]: one mixed-precision multiply with an
+// fp16 result (v_fma_mix) per element, rounded once.
+DEVI bf16x8 cvt_f16x8_mul(const f32x16 &x, int at, float m) {
+    f16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = static_cast<_Float16>(x[at + j] * m);
+    return __builtin_bit_cast(bf16x8, h);
+}
+DEVI bf16x8 cvt_f16x8_prod(const f32x16 &x, const f32x16 &y, int at) {
+    f16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = static_cast<_Float16>(x[at + j] * y[at + j]);
+    return __builtin_bit_cast(bf16x8, h);
+}
+// Their rounding errors, x m - hi and x y - hi (the products in float32), rounded to fp16.
+DEVI bf16x8 cvt_f16x8_mul_lo(const f32x16 &x, int at, float m, bf16x8 hi) {
+    const f16x8 h = __builtin_bit_cast(f16x8, hi);
+    f16x8 l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) l[j] = static_cast<_Float16>(x[at + j] * m - static_cast<float>(h[j]));
+    return __builtin_bit_cast(bf16x8, l);
+}
+DEVI bf16x8 cvt_f16x8_prod_lo(const f32x16 &x, const f32x16 &y, int at, bf16x8 hi) {
+    const f16x8 h = __builtin_bit_cast(f16x8, hi);
+    f16x8 l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) l[j] = static_cast<_Float16>(x[at + j] * y[at + j] - static_cast<float>(h[j]));
+    return __builtin_bit_cast(bf16x8, l);
+}
 
 // Row index (within a 32-row MFMA tile) that accumulator register r of this lane holds.
 DEVI int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }

@@ -367,29 +367,48 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     };
 
     // PV(t-1) first, then S(t): P's registers are dead before S is written, so the two share
-    // registers.
+    // registers.  PV runs in groups of 16 keys (sub-tile kt = grp / 2, half u = grp % 2); a
+    // group's V^T fragments are read while the previous group's MFMAs run (only this group's
+    // wave issues MFMAs on its SIMD in this phase, so a read waited for right before its MFMA
+    // stalls the SIMD).  A sub-tile with no key this wave's queries see (past the diagonal or
+    // past S) enters too, as straight-line code: its P is exactly 0 (scores at -inf) and its V
+    // rows are finite (rows past S are zero-filled), so it adds nothing.
     auto gemm = [&](int t) {
         if (t > t_begin && sub_live(t - 1, 0)) {
             const u32x4 *vt_ = sm[(t - 1) & 1].v;
+            constexpr int NG = 2 * NT;
+            constexpr int MF = F16V ? NDT : 2 * NDT;  // MFMAs per group
+            constexpr int RPM = 2 * NDT / MF;         // V^T reads per MFMA
+            bf16x8 va[2][NDT];
+            auto load_v = [&](int grp) {
 #pragma unroll
-            for (int kt = 0; kt < NT; ++kt) {
-                if (kt > 0 && !sub_live(t - 1, kt)) continue;
+                for (int dt = 0; dt < NDT; ++dt) va[grp & 1][dt] = tr_frag<kBN, D>(vt_, trb, 16 * grp, dt);
+            };
+            load_v(0);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    bf16x8 va[NDT];
+            for (int grp = 0; grp < NG; ++grp) {
+                if (grp + 1 < NG) load_v(grp + 1);
+                const int kt = grp >> 1, u = grp & 1;
+                if constexpr (F16V) {
 #pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) va[dt] = tr_frag<kBN, D>(vt_, trb, kt * 32 + 16 * u, dt);
-                    if constexpr (F16V) {
+                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_f16(va[grp & 1][dt], ph[kt][u], oacc[dt]);
+                } else {
 #pragma unroll
-                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_f16(va[dt], ph[kt][u], oacc[dt]);
-                    } else {
+                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[grp & 1][dt], ph[kt][u], oacc[dt]);
 #pragma unroll
-                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], ph[kt][u], oacc[dt]);
-#pragma unroll
-                        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[dt], pl[kt][u], oacc[dt]);
-                    }
+                    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma_bf16(va[grp & 1][dt], pl[kt][u], oacc[dt]);
                 }
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * NDT, 0);  // group 0's reads
+#pragma unroll
+            for (int grp = 0; grp + 1 < NG; ++grp)
+#pragma unroll
+                for (int i = 0; i < MF; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // an MFMA of this group
+                    __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);  // reads of the next
+                }
+            __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (t < t_end && sub_live(t, 0)) {
             const u32x4 *kt_ = sm[t & 1].k;
