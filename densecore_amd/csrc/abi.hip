@@ -135,7 +135,8 @@ dc_status launched(hipError_t e) {
 size_t fwd_order_ws(const dc::AttnShape &s) { return round_up((size_t)2 * s.B * s.H * sizeof(int)); }
 size_t fwd_v16_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * s.S * s.E * 2); }
 size_t fwd_partial_ws(const dc::AttnShape &s) {
-    return round_up((size_t)s.B * s.Hkv * dc::f16_parts((int64_t)s.B * s.Hkv, (int64_t)s.S * s.E) * sizeof(float));
+    const dc::F16Copy v{nullptr, nullptr, (int64_t)s.S * s.E, nullptr};
+    return round_up(dc::f16_partial_floats((int64_t)s.B * s.Hkv, &v, 1) * sizeof(float));
 }
 size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
@@ -174,12 +175,13 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
         const size_t nq = (size_t)s.B * s.H * s.L * s.E, nk = (size_t)s.B * s.Hkv * s.S * s.E;
         const int64_t qslab = (int64_t)s.repeat * s.L * s.E, kslab = (int64_t)s.S * s.E;
         const int64_t nslabs = (int64_t)s.B * s.Hkv;
-        const int parts = std::max(dc::f16_parts(nslabs, qslab), dc::f16_parts(nslabs, kslab));
+        const dc::F16Copy sizes[4] = {{nullptr, nullptr, qslab, nullptr}, {nullptr, nullptr, kslab, nullptr},
+                                      {nullptr, nullptr, kslab, nullptr}, {nullptr, nullptr, qslab, nullptr}};
         l.q16 = take(nq * 2);
         l.do16 = take(nq * 2);
         l.k16 = take(nk * 2);
         l.v16 = take(nk * 2);
-        l.partial = take((size_t)s.B * s.Hkv * parts * sizeof(float));
+        l.partial = take(dc::f16_partial_floats(nslabs, sizes, 4) * sizeof(float));  // all four copies' maxima
         l.exps = take((size_t)4 * s.B * s.Hkv * sizeof(int));
         l.copies_end = at;
         l.split = take(dc::bwd_bf16_split_bytes(s));

@@ -803,10 +803,11 @@ hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     record_schedule(f16_products, 1);
     const int64_t n = (int64_t)a.s.B * a.s.Hkv;
     const int64_t qslab = (int64_t)a.s.repeat * a.s.L * a.s.E, kslab = (int64_t)a.s.S * a.s.E;
-    return_if(launch_to_f16(a.q, a.q16, n, qslab, a.f16_partial, a.exps, st));
-    return_if(launch_to_f16(a.k, a.k16, n, kslab, a.f16_partial, a.exps + n, st));
-    return_if(launch_to_f16(a.v, a.v16, n, kslab, a.f16_partial, a.exps + 2 * n, st));
-    return_if(launch_to_f16(a.dout, a.do16, n, qslab, a.f16_partial, a.exps + 3 * n, st));
+    const F16Copy copies[4] = {{a.q, a.q16, qslab, a.exps},
+                               {a.k, a.k16, kslab, a.exps + n},
+                               {a.v, a.v16, kslab, a.exps + 2 * n},
+                               {a.dout, a.do16, qslab, a.exps + 3 * n}};
+    return_if(launch_to_f16(copies, 4, n, a.f16_partial, st));
     BwdArgs f = a;
     f.q = a.q16, f.k = a.k16, f.v = a.v16, f.dout = a.do16;
     if (a.split) {

@@ -14,7 +14,8 @@
 //
 // Two passes: slab_max_kernel reduces each of `parts` segments (of `per` elements) of a slab to
 // its largest finite magnitude; slab_convert_kernel reads a slab's partial maxima, derives e
-// (written once per slab) and converts its segment.
+// (written once per slab) and converts its segment.  Each pass is one launch for all the
+// tensors a call copies (the backward's four): its blocks are dealt to the tensors in order.
 #include <cmath>
 
 #include "common.hpp"
@@ -37,12 +38,38 @@ DEVI void segment(int64_t slab, int64_t per, int p, int64_t *begin, int64_t *end
     *end = *begin + per < slab ? *begin + per : slab;
 }
 
-__global__ __launch_bounds__(kThreads) void slab_max_kernel(const uint16_t *src, int64_t slab, int parts,
-                                                            int64_t per, bool vec, float *partial) {
-    const int s = blockIdx.x / parts, p = blockIdx.x % parts;
+// The tensors of one launch: copy j has nslabs slabs of slab[j] elements, cut into parts[j]
+// segments of per[j]; its blocks are [first[j], first[j + 1]).
+struct SlabJobs {
+    const uint16_t *src[kMaxF16Copies];
+    _Float16 *dst[kMaxF16Copies];
+    float *partial[kMaxF16Copies];
+    int *exps[kMaxF16Copies];
+    int64_t slab[kMaxF16Copies], per[kMaxF16Copies];
+    int parts[kMaxF16Copies];
+    bool vec[kMaxF16Copies];
+    int first[kMaxF16Copies + 1];
+    int n;
+};
+
+// The copy j of launch-wide block `idx` and its block index within that copy (wave-uniform).
+DEVI int job_of(const SlabJobs &J, int idx, int *local) {
+    int j = 0;
+    while (j + 1 < J.n && idx >= J.first[j + 1]) ++j;
+    *local = idx - J.first[j];
+    return j;
+}
+
+__global__ __launch_bounds__(kThreads) void slab_max_kernel(SlabJobs J) {
+    int b;
+    const int j = job_of(J, (int)blockIdx.x, &b);
+    const int64_t slab = J.slab[j], per = J.per[j];
+    const int parts = J.parts[j];
+    const bool vec = J.vec[j];
+    const int s = b / parts, p = b % parts;
     int64_t i0, i1;
     segment(slab, per, p, &i0, &i1);
-    const uint16_t *x = src + (int64_t)s * slab;
+    const uint16_t *x = J.src[j] + (int64_t)s * slab;
     float m = 0.f;
     if (vec) {  // segments start at multiples of 8 elements (slab % 8 == 0, per % 8 == 0)
 #pragma unroll 4
@@ -63,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void slab_max_kernel(const uint16_t *src,
         float r = wm[0];
 #pragma unroll
         for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, wm[w]);
-        partial[blockIdx.x] = r;
+        J.partial[j][b] = r;
     }
 }
 
@@ -75,10 +102,16 @@ DEVI int slab_exp(float m) {
     return 15 - k;
 }
 
-__global__ __launch_bounds__(kThreads) void slab_convert_kernel(const uint16_t *src, _Float16 *dst, int64_t slab,
-                                                                int parts, int64_t per, bool vec,
-                                                                const float *partial, int *exps) {
-    const int s = blockIdx.x / parts, p = blockIdx.x % parts;
+// Blocks run in reverse order of the max pass's: the data that pass read last is the most likely
+// to be still in the caches (four tensors exceed the 256 MB last-level cache).
+__global__ __launch_bounds__(kThreads) void slab_convert_kernel(SlabJobs J) {
+    int b;
+    const int j = job_of(J, (int)(gridDim.x - 1 - blockIdx.x), &b);
+    const int64_t slab = J.slab[j], per = J.per[j];
+    const int parts = J.parts[j];
+    const bool vec = J.vec[j];
+    const float *partial = J.partial[j];
+    const int s = b / parts, p = b % parts;
     // The slab's largest finite magnitude: its `parts` partial maxima, reduced by the block.
     float m = 0.f;
     for (int j = threadIdx.x; j < parts; j += kThreads) m = fmaxf(m, partial[(int64_t)s * parts + j]);
@@ -90,11 +123,11 @@ __global__ __launch_bounds__(kThreads) void slab_convert_kernel(const uint16_t *
 #pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) m = fmaxf(m, wm[w]);
     const int e = slab_exp(m);
-    if (p == 0 && threadIdx.x == 0) exps[s] = e;
+    if (p == 0 && threadIdx.x == 0) J.exps[j][s] = e;
     int64_t i0, i1;
     segment(slab, per, p, &i0, &i1);
-    const uint16_t *x = src + (int64_t)s * slab;
-    _Float16 *y = dst + (int64_t)s * slab;
+    const uint16_t *x = J.src[j] + (int64_t)s * slab;
+    _Float16 *y = J.dst[j] + (int64_t)s * slab;
     auto cvt = [&](uint16_t bits) {
         return static_cast<_Float16>(ldexpf(__uint_as_float((uint32_t)bits << 16), e));
     };
@@ -133,17 +166,38 @@ int f16_parts(int64_t nslabs, int64_t slab) {
     return (int)(parts < 1 ? 1 : parts);
 }
 
-hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t slab, float *partial, int *exps,
-                         hipStream_t st) {
-    if (nslabs == 0 || slab == 0) return hipSuccess;
-    const int64_t per = f16_segment(nslabs, slab);
-    const int parts = f16_parts(nslabs, slab);
-    const bool vec = slab % 8 == 0 && per % 8 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0;
-    const dim3 grid((unsigned)(nslabs * parts)), block(kThreads);
-    return_if(launch(slab_max_kernel, grid, block, st, static_cast<const uint16_t *>(src), slab, parts, per, vec,
-                     partial));
-    return launch(slab_convert_kernel, grid, block, st, static_cast<const uint16_t *>(src),
-                  static_cast<_Float16 *>(dst), slab, parts, per, vec, static_cast<const float *>(partial), exps);
+size_t f16_partial_floats(int64_t nslabs, const F16Copy *copies, int n) {
+    size_t total = 0;
+    for (int j = 0; j < n; ++j) total += (size_t)nslabs * f16_parts(nslabs, copies[j].slab);
+    return total;
+}
+
+hipError_t launch_to_f16(const F16Copy *copies, int n, int64_t nslabs, float *partial, hipStream_t st) {
+    SlabJobs J{};
+    J.first[0] = 0;
+    float *at = partial;
+    for (int j = 0; j < n; ++j) {
+        const F16Copy &c = copies[j];
+        const int64_t slab = nslabs > 0 ? c.slab : 0;
+        const int parts = slab > 0 ? f16_parts(nslabs, slab) : 0;
+        J.src[J.n] = static_cast<const uint16_t *>(c.src);
+        J.dst[J.n] = static_cast<_Float16 *>(c.dst);
+        J.exps[J.n] = c.exps;
+        J.slab[J.n] = slab;
+        J.per[J.n] = slab > 0 ? f16_segment(nslabs, slab) : 1;
+        J.parts[J.n] = parts;
+        J.vec[J.n] = slab % 8 == 0 && J.per[J.n] % 8 == 0 && ((uintptr_t)c.src & 15) == 0 &&
+                     ((uintptr_t)c.dst & 15) == 0;
+        J.partial[J.n] = at;
+        if (slab == 0) continue;  // nothing to copy: the copy takes no blocks
+        at += nslabs * parts;
+        J.first[J.n + 1] = J.first[J.n] + (int)(nslabs * parts);
+        ++J.n;
+    }
+    if (J.n == 0) return hipSuccess;
+    const dim3 grid((unsigned)J.first[J.n]), block(kThreads);
+    return_if(launch(slab_max_kernel, grid, block, st, J));
+    return launch(slab_convert_kernel, grid, block, st, J);
 }
 
 }  // namespace dc

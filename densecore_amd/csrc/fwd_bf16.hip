@@ -581,8 +581,8 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
         if (a.v16) {
             record_schedule(f16_products, 1);
             FwdArgs f = a;
-            return_if(launch_to_f16(a.v, a.v16, (int64_t)a.s.B * a.s.Hkv, (int64_t)a.s.S * a.s.E,
-                                    a.f16_partial, a.vexp, st));
+            const F16Copy vcopy{a.v, a.v16, (int64_t)a.s.S * a.s.E, a.vexp};
+            return_if(launch_to_f16(&vcopy, 1, (int64_t)a.s.B * a.s.Hkv, a.f16_partial, st));
             f.v = a.v16;
             if (a.split_o) {
                 const FwdSplitPlan p = plan<D>(a.s);

@@ -125,8 +125,19 @@ int device_occupancy(const void *kernel, int threads);
 
 // bf16 -> fp16 copies scaled per slab (f16_stage.hip): segments per slab, and the two passes.
 int f16_parts(int64_t nslabs, int64_t slab);
-hipError_t launch_to_f16(const void *src, void *dst, int64_t nslabs, int64_t slab, float *partial, int *exps,
-                         hipStream_t st);
+// One tensor to copy: nslabs slabs of `slab` elements (the count is shared by the launch),
+// exponents to exps[0 .. nslabs).
+constexpr int kMaxF16Copies = 4;
+struct F16Copy {
+    const void *src;
+    void *dst;
+    int64_t slab;
+    int *exps;
+};
+// Floats of per-segment maxima that launch_to_f16 needs for these copies.
+size_t f16_partial_floats(int64_t nslabs, const F16Copy *copies, int n);
+// Up to kMaxF16Copies tensors in two launches (all maxima, then all conversions).
+hipError_t launch_to_f16(const F16Copy *copies, int n, int64_t nslabs, float *partial, hipStream_t st);
 
 // Each launcher returns hipSuccess or the launch error; it never synchronizes.
 hipError_t launch_fwd_f32(const FwdArgs &a, hipStream_t st);
