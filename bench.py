@@ -5,9 +5,11 @@
 A step is one pass of the hot path over one batch of synthetic, HBM-resident input:
 C2 (the headline) is causal fp32 forward + backward at B8 H12 T1024
 D64 through the C ABI (dc_sdpa_fwd then dc_sdpa_bwd).  ``value`` is C2's algorithmic TFLOP/s
-(4*B*H*T^2*D/2 forward, 2.5x that backward).  The same line carries the decode figure the
+(4*B*H*T^2*D/2 forward, 2.5x that backward), after exactly W untimed steps.  The same line
+carries the decode figure the
 metric names (C4, dc_sdpa_decode, GB/s of K + V + q + out + lse), the other configurations'
-throughput (wall clock over K steps between two synchronizations), a roofline entry per
+throughput (wall clock over K steps between two synchronizations, each config warmed up for at
+least W steps and 100 ms of its own work, so that it is timed at steady clocks), a roofline entry per
 entry point whose kernel time comes from HIP events on the launch stream around back-to-back
 calls of that entry point alone, and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
 ``math_path`` reports the composed path's own kernels (softmax forward/backward, the Bernoulli
@@ -50,6 +52,27 @@ def load_traffic():
         with open(path) as f:
             return json.load(f)
     return {}
+
+
+# Secondary configs warm up for at least this long (and at least --warmup steps): after the host
+# has built a config's inputs the GPU has idled and its clock has dropped, and a few steps of a
+# 50 us config do not bring it back.  The headline C2 step takes exactly --warmup steps.
+MIN_WARMUP_MS = 100.0
+
+
+def warm_up(torch, fn, steps, headline):
+    """Run ``fn`` untimed: ``steps`` times, and for secondary configs until MIN_WARMUP_MS of it
+    has run."""
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    if headline:
+        return
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < MIN_WARMUP_MS:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
 
 
 def kernel_ms(torch, stream, fn, n):
@@ -136,9 +159,7 @@ def bench_prefill(torch, native, name, steps, warmup, dev):
         if bwd:
             native._flash_attention_backward(g, q, k, v, out, lse, causal, scale, mask)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(torch, step, warmup, headline=name == "C2")
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
@@ -206,9 +227,7 @@ def bench_decode(torch, native, steps, warmup, dev):
     q, k, v = (torch.from_numpy(d[n]).to(dev) for n in "qkv")
     del d
     stream = torch.cuda.current_stream(dev)
-    for _ in range(warmup):
-        native._flash_decode(q, k, v)
-    torch.cuda.synchronize()
+    warm_up(torch, lambda: native._flash_decode(q, k, v), warmup, headline=False)
     t0 = time.perf_counter()
     for _ in range(steps):
         native._flash_decode(q, k, v)
@@ -242,8 +261,7 @@ def bench_math(torch, steps, warmup, dev):
     y = native._softmax(x, mask, True)
     g = torch.randn_like(x)
     reps = max(steps, 10)
-    for _ in range(warmup):
-        native._softmax(x, mask, True)
+    warm_up(torch, lambda: native._softmax(x, mask, True), warmup, headline=False)
     res = {"workload": "C3 shape B16 H16 L=S=512, key-padding mask, dropout p=0.1",
            "timing_calls": reps}
     ms = kernel_ms(torch, stream, lambda: native._softmax(x, mask, True), reps)

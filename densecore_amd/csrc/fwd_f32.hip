@@ -462,6 +462,45 @@ __global__ __launch_bounds__(1024) void rowmask_order_kernel(FwdArgs a, int ntil
     for (int i = tid; i < BH; i += 1024) a.order[atomicAdd(&start[a.tiles[i]], 1)] = i;
 }
 
+// Masks that depend on the batch and the key only (head and query strides 0: key padding, C3):
+// one launch instead of the two above.  One workgroup counts the live tiles of each batch's mask
+// row, a wave per row, and sorts the heads by their batch's count, descending.
+template <int BN>
+__global__ __launch_bounds__(1024) void rowmask_batch_order_kernel(FwdArgs a, int ntiles) {
+    static_assert(BN == 32 || BN == 64, "one or two tiles per wave-wide pass");
+    __shared__ int count[kOrderMaxBatch];
+    __shared__ int start[kOrderMaxTiles + 1];
+    const AttnShape &s = a.s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int v = tid; v <= ntiles; v += 1024) start[v] = 0;
+    for (int b = wave; b < s.B; b += 16) {
+        const float *row = s.mask + (int64_t)b * s.msb;
+        int c = 0;
+#pragma unroll 4
+        for (int k0 = 0; k0 < s.S; k0 += 64) {
+            const int key = k0 + lane;
+            const uint64_t live = __ballot(key < s.S && row[key] != -INFINITY);
+            if (BN == 64) c += live != 0;
+            else c += ((live & 0xffffffffull) != 0) + ((live >> 32) != 0);
+        }
+        if (lane == 0) count[b] = c;
+    }
+    __syncthreads();
+    const int BH = s.B * s.H;
+    for (int i = tid; i < BH; i += 1024) atomicAdd(&start[count[i / s.H]], 1);
+    __syncthreads();
+    if (tid == 0) {  // start[v] = number of heads with more live tiles than v
+        int run = 0;
+        for (int v = ntiles; v >= 0; --v) {
+            const int c = start[v];
+            start[v] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < BH; i += 1024) a.order[atomicAdd(&start[count[i / s.H]], 1)] = i;
+}
+
 // The split of this instantiation's grid on the current device (fwd_split.hpp).
 template <int D, int BN, int W>
 FwdSplitPlan plan(const AttnShape &s) {
@@ -507,8 +546,12 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
         else if (mask && a.s.msl == 0 && BN <= 64) {
             const int ntiles = (a.s.S + BN - 1) / BN;
             if (a.order && a.s.B * a.s.H <= kOrderMaxHeads && ntiles <= kOrderMaxTiles) {
-                return_if(launch(rowmask_tiles_kernel<BN>, dim3(a.s.B * a.s.H), dim3(64), st, a));
-                return_if(launch(rowmask_order_kernel, dim3(1), dim3(1024), st, a, ntiles));
+                if (a.s.msh == 0 && a.s.B <= kOrderMaxBatch) {
+                    return_if(launch(rowmask_batch_order_kernel<BN>, dim3(1), dim3(1024), st, a, ntiles));
+                } else {
+                    return_if(launch(rowmask_tiles_kernel<BN>, dim3(a.s.B * a.s.H), dim3(64), st, a));
+                    return_if(launch(rowmask_order_kernel, dim3(1), dim3(1024), st, a, ntiles));
+                }
                 const dim3 ogrid(nqt * 8 * ((a.s.B * a.s.H + 7) / 8));
                 return_if(launch(fwd_f32_kernel<D, BN, W, false, true, true, true>, ogrid, block, st, a));
             } else {

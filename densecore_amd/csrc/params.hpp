@@ -45,6 +45,7 @@ struct FwdArgs {
 // the grid is small enough for one workgroup to sort.
 constexpr int kOrderMaxHeads = 65536;
 constexpr int kOrderMaxTiles = 1024;
+constexpr int kOrderMaxBatch = 1024;  // batch rows of the one-launch order (key-padding masks)
 
 struct BwdArgs {
     AttnShape s;
