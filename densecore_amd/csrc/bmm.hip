@@ -111,12 +111,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int bt = w / per, r = w % per, m0 = (r / nt) * BM, n0 = (r % nt) * BN;
     const float *ap = g.a + (int64_t)bt * g.sab;
     const float *bp = g.b + (int64_t)bt * g.sbb;
+    // Causal products: the largest query index among rows [r0, r1] of the block (rows across a
+    // head boundary: L - 1).
+    auto max_query = [&](int r0, int r1) {
+        const int64_t j0 = (int64_t)g.causal_row0 + r0, j1 = (int64_t)g.causal_row0 + r1;
+        return j0 / g.causal_L != j1 / g.causal_L ? g.causal_L - 1 : (int)(j1 % g.causal_L);
+    };
+    int kk = g.k;
+    if (g.causal_mode == 1 && n0 > max_query(m0, min(m0 + BM, g.m) - 1)) return;  // no key visible
+    if (g.causal_mode == 2) kk = min(kk, max_query(m0, min(m0 + BM, g.m) - 1) + 1);
+    const int nk = (kk + BK - 1) / BK;
+    // The first k tile at or after kt that contributes (mode 3: some row of it sees key m0).
+    auto next_live = [&](int kt) {
+        if (g.causal_mode == 3)
+            while (kt < nk && max_query(kt * BK, min((kt + 1) * BK, g.k) - 1) < m0) ++kt;
+        return kt;
+    };
 
     Stage<BM, LA> sa;
     Stage<BN, LB> sb;
+    int kt = next_live(0);
     // B's "rows" are its n columns: its row stride is the n stride, its k stride the k stride.
-    sa.load(ap, g.sam, g.sak, m0, g.m, 0, g.k, tid);
-    sb.load(bp, g.sbn, g.sbk, n0, g.n, 0, g.k, tid);
+    sa.load(ap, g.sam, g.sak, m0, g.m, kt * BK, kk, tid);
+    sb.load(bp, g.sbn, g.sbk, n0, g.n, kt * BK, kk, tid);
     sa.store(sm.a[0], tid);
     sb.store(sm.b[0], tid);
     __syncthreads();
@@ -129,12 +146,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    const int nk = (g.k + BK - 1) / BK;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) {
-            sa.load(ap, g.sam, g.sak, m0, g.m, (kt + 1) * BK, g.k, tid);
-            sb.load(bp, g.sbn, g.sbk, n0, g.n, (kt + 1) * BK, g.k, tid);
+    for (int buf = 0; kt < nk; buf ^= 1) {
+        const int next = next_live(kt + 1);
+        if (next < nk) {
+            sa.load(ap, g.sam, g.sak, m0, g.m, next * BK, kk, tid);
+            sb.load(bp, g.sbn, g.sbk, n0, g.n, next * BK, kk, tid);
         }
         const float(*ta)[BM + kPad] = sm.a[buf];
         const float(*tb)[BN + kPad] = sm.b[buf];
@@ -150,11 +166,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
                 for (int j = 0; j < TN; ++j) acc[i][j] = mfma_f32(fa[i], fb[j], acc[i][j]);
         }
-        if (kt + 1 < nk) {
+        if (next < nk) {
             sa.store(sm.a[buf ^ 1], tid);
             sb.store(sm.b[buf ^ 1], tid);
         }
         __syncthreads();
+        kt = next;
     }
 
     float *cp = g.c + (int64_t)bt * g.scb;

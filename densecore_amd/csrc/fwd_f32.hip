@@ -476,7 +476,6 @@ __global__ __launch_bounds__(1024) void rowmask_batch_order_kernel(FwdArgs a, in
     for (int b = wave; b < s.B; b += 16) {
         const float *row = s.mask + (int64_t)b * s.msb;
         int c = 0;
-#pragma unroll 4
         for (int k0 = 0; k0 < s.S; k0 += 64) {
             const int key = k0 + lane;
             const uint64_t live = __ballot(key < s.S && row[key] != -INFINITY);

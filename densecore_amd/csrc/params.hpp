@@ -107,6 +107,14 @@ struct BmmArgs {
     int64_t sbb, sbk, sbn;  // B's strides: batch, k, n
     int64_t scb, scm;       // C's strides: batch, m (unit stride along n)
     bool acc;               // C += A B (else C = A B)
+    // Causal attention products of the materialized path (wide.hip); 0 for a plain product.  The
+    // m index is row causal_row0 + m of an item whose rows are queries j % causal_L (heads of L
+    // rows each), keys are visible up to the query index.  1: n is the key index (scores):
+    // tiles whose keys all lie past every query of the tile are skipped, C left unwritten there.
+    // 2: k is the key index (P V, dS K): the k loop stops after the tile's last visible key.
+    // 3: m is the key index and k the block's rows (P^T dO, dS^T Q): k tiles whose rows all see
+    // none of the tile's keys are skipped.
+    int causal_mode, causal_L, causal_row0;
 };
 hipError_t launch_bmm(const BmmArgs &g, hipStream_t st);
 

@@ -104,6 +104,40 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void wide_softmax_kernel(WideRo
     if (lane == 0) w.lse_out[r.bhl] = lse;
 }
 
+// The same with the row in registers (NV values per lane, rows of at most 64 NV keys): one read
+// and one write of the row instead of three reads and two writes.
+template <int NV>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void wide_softmax_reg_kernel(WideRows w) {
+    const int64_t g = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (g >= (int64_t)w.s.B * w.s.Hkv * w.rows) return;  // whole waves exit together
+    const int lane = threadIdx.x & 63, S = w.s.S;
+    const RowId r = row_id(w, g);
+    const float *mrow = mask_row(w, r);
+    float *x = w.x + g * S;
+    float v[NV];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int key = 64 * i + lane;
+        v[i] = key < S ? score(w, r, mrow, key, x[key]) : -INFINITY;
+        mx = fmaxf(mx, v[i]);
+    }
+    mx = wave_max(mx);
+    float lse = 0.f;
+    if (mx != -INFINITY) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) sum += expf(v[i] - mx);
+        lse = mx + logf(wave_sum(sum));
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int key = 64 * i + lane;
+        if (key < S) x[key] = mx == -INFINITY ? 0.f : expf(v[i] - lse);
+    }
+    if (lane == 0) w.lse_out[r.bhl] = lse;
+}
+
 // Backward: P = exp(scale * S + mask - lse) (causal keys past the query: 0).
 __global__ __launch_bounds__(64 * kRowsPerBlock) void wide_p_kernel(WideRows w) {
     const int64_t g = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
@@ -125,7 +159,10 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void wide_ds_kernel(WideRows w)
     const float dsum = w.dsum[r.bhl];
     const float *p = w.x + g * S;
     float *y = w.y + g * S;
-    for (int key = lane; key < S; key += 64) y[key] = w.s.scale * (p[key] * (y[key] - dsum));
+    // Keys past the query (causal) get 0 without reading dP: its tiles past the diagonal are
+    // not computed (the score products skip them).
+    for (int key = lane; key < S; key += 64)
+        y[key] = w.s.causal && key > r.l ? 0.f : w.s.scale * (p[key] * (y[key] - dsum));
 }
 
 template <typename Src, typename Dst>
@@ -156,14 +193,17 @@ hipError_t zero(float *p, int64_t n, hipStream_t st) {
 }
 
 // One batched product over the items of a row block: C (+)= A B, m x k times k x n.
+// causal: 0, or the mode of BmmArgs::causal_mode for a product over the block's rows (row0 + m,
+// or row0 + k in mode 3, of each item); taken only for causal attention.
 hipError_t product(int items, int m, int n, int k, const float *a, int64_t sab, int64_t sam, int64_t sak,
                    const float *b, int64_t sbb, int64_t sbk, int64_t sbn, float *c, int64_t scb, int64_t scm,
-                   bool acc, hipStream_t st) {
+                   bool acc, hipStream_t st, int causal = 0, const AttnShape *s = nullptr, int64_t row0 = 0) {
     BmmArgs g{};
     g.a = a, g.b = b, g.c = c;
     g.batch = items, g.m = m, g.n = n, g.k = k;
     g.sab = sab, g.sam = sam, g.sak = sak, g.sbb = sbb, g.sbk = sbk, g.sbn = sbn;
     g.scb = scb, g.scm = scm, g.acc = acc;
+    if (causal && s && s->causal && s->L > 0) g.causal_mode = causal, g.causal_L = s->L, g.causal_row0 = (int)row0;
     return launch_bmm(g, st);
 }
 
@@ -234,16 +274,22 @@ hipError_t launch_wide_fwd(const FwdArgs &a, bool bf16, void *ws, size_t bytes, 
     for (int64_t row0 = 0; row0 < g.M; row0 += R) {
         const int rows = (int)(g.M - row0 < R ? g.M - row0 : R);
         // S = Q K^T (K^T: the transposed view of k)
+        // (causal: tiles whose keys all lie past their queries are skipped; the softmax never
+        // reads those scores)
         return_if(product((int)g.items, rows, S, E, q + row0 * E, ME, E, 1, k, SE, 1, E, sbuf, (int64_t)rows * S, S,
-                          false, st));
+                          false, st, 1, &s, row0));
         WideRows w{};
         w.s = s, w.x = sbuf, w.lse_out = a.lse, w.row0 = (int)row0, w.rows = rows;
         const int64_t nrows = g.items * rows;
-        return_if(launch(wide_softmax_kernel, dim3((unsigned)((nrows + kRowsPerBlock - 1) / kRowsPerBlock)),
-                         dim3(64 * kRowsPerBlock), st, w));
-        // O = P V
+        const dim3 rgrid((unsigned)((nrows + kRowsPerBlock - 1) / kRowsPerBlock)), rblock(64 * kRowsPerBlock);
+        if (S <= 512) return_if(launch(wide_softmax_reg_kernel<8>, rgrid, rblock, st, w));
+        else if (S <= 1024) return_if(launch(wide_softmax_reg_kernel<16>, rgrid, rblock, st, w));
+        else if (S <= 2048) return_if(launch(wide_softmax_reg_kernel<32>, rgrid, rblock, st, w));
+        else if (S <= 4096) return_if(launch(wide_softmax_reg_kernel<64>, rgrid, rblock, st, w));
+        else return_if(launch(wide_softmax_kernel, rgrid, rblock, st, w));
+        // O = P V (causal: keys up to each row tile's last query)
         return_if(product((int)g.items, rows, E, S, sbuf, (int64_t)rows * S, S, 1, v, SE, E, 1, out + row0 * E, ME,
-                          E, false, st));
+                          E, false, st, 2, &s, row0));
     }
     if (bf16) return_if((cast<float, __bf16>(out, a.out, g.nq, st)));
     return hipSuccess;
@@ -293,16 +339,17 @@ hipError_t launch_wide_bwd(const BwdArgs &a, bool bf16, void *ws, size_t bytes, 
         w.s = s, w.x = sbuf, w.y = pbuf, w.lse_in = a.lse, w.dsum = a.dsum, w.row0 = (int)row0, w.rows = rows;
         const dim3 rgrid((unsigned)((g.items * rows + kRowsPerBlock - 1) / kRowsPerBlock)), rblock(64 * kRowsPerBlock);
         // S = Q K^T, then P in place
-        return_if(product((int)g.items, rows, S, E, qb, ME, E, 1, k, SE, 1, E, sbuf, RS, S, false, st));
+        return_if(product((int)g.items, rows, S, E, qb, ME, E, 1, k, SE, 1, E, sbuf, RS, S, false, st, 1, &s, row0));
         return_if(launch(wide_p_kernel, rgrid, rblock, st, w));
         // dV += P^T dO (P^T: the transposed view of the block's P)
-        return_if(product((int)g.items, S, E, rows, sbuf, RS, 1, S, ob, ME, E, 1, dv, SE, E, true, st));
+        return_if(product((int)g.items, S, E, rows, sbuf, RS, 1, S, ob, ME, E, 1, dv, SE, E, true, st, 3, &s, row0));
         // dP = dO V^T, then dS = scale P (dP - dsum) in place
-        return_if(product((int)g.items, rows, S, E, ob, ME, E, 1, v, SE, 1, E, pbuf, RS, S, false, st));
+        return_if(product((int)g.items, rows, S, E, ob, ME, E, 1, v, SE, 1, E, pbuf, RS, S, false, st, 1, &s, row0));
         return_if(launch(wide_ds_kernel, rgrid, rblock, st, w));
         // dQ = dS K (the block's rows), dK += dS^T Q
-        return_if(product((int)g.items, rows, E, S, pbuf, RS, S, 1, k, SE, E, 1, dq + row0 * E, ME, E, false, st));
-        return_if(product((int)g.items, S, E, rows, pbuf, RS, 1, S, qb, ME, E, 1, dk, SE, E, true, st));
+        return_if(product((int)g.items, rows, E, S, pbuf, RS, S, 1, k, SE, E, 1, dq + row0 * E, ME, E, false, st, 2,
+                          &s, row0));
+        return_if(product((int)g.items, S, E, rows, pbuf, RS, 1, S, qb, ME, E, 1, dk, SE, E, true, st, 3, &s, row0));
     }
     if (bf16) {
         return_if((cast<float, __bf16>(dq, a.dq, g.nq, st)));
