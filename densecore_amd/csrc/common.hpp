@@ -203,6 +203,17 @@ DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
 // s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
 DEVI void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// s_waitcnt vmcnt(N): all but the N most recently issued global loads of this wave are done
+// (they complete in issue order).  N < 64: its low four bits go in [3:0], the rest in [15:14].
+template <int N>
+DEVI void wait_vmem_but() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned its data.
+DEVI void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
 // Scheduling hint for a straight run of NMFMA MFMAs, each consuming R LDS reads issued in the
 // same block: the reads are kept AHEAD MFMAs in front of their use (the compiler otherwise
 // issues each read just before its MFMA and exposes the LDS latency on every one).

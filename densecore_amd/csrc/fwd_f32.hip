@@ -26,7 +26,7 @@
 namespace dc {
 namespace {
 
-// W waves per workgroup, 32 queries per wave (4, or 2 for short causal problems).
+// W waves per workgroup, 32 queries per wave (4; 2 or 1 for short causal problems).
 
 template <int D, int BN>
 struct alignas(16) FwdSmem {
@@ -97,9 +97,14 @@ DEVI int swz(int row) {
     return (row ^ ((row & 4) << 1)) & (D / 4 - 1);
 }
 
-// Issue this wave's share of tile [n0, n0 + BN) into buffer `buf` (keys past the end read a
-// valid row, S - 1; their scores are -inf, so they contribute nothing).
+// Global loads per wave for one K (or V) tile: each wave-wide load fills 64 / (D / 4) rows.
 template <int D, int BN, int W>
+constexpr int kTileLoads = BN / W / (64 / (D / 4));
+
+// Issue this wave's share of tile [n0, n0 + BN) into buffer `buf`: K and V, or only one of
+// them (keys past the end read a valid row, S - 1; their scores are -inf, so they contribute
+// nothing).
+template <int D, int BN, int W, bool DO_K = true, bool DO_V = true>
 DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, int n0, int S,
                      int wave, int lane) {
     constexpr int C = D / 4;             // 16-byte chunks per row
@@ -112,8 +117,8 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
         const int row = r0 + lane / C;
         const int chunk = (lane % C) ^ swz<D>(row);  // logical chunk stored at this slot
         const int64_t off = (int64_t)min(n0 + row, S - 1) * D + chunk * 4;
-        lds_dma16(kb + off, &sm.k[r0][0]);
-        lds_dma16(vb + off, &sm.v[r0][0]);
+        if constexpr (DO_K) lds_dma16(kb + off, &sm.k[r0][0]);
+        if constexpr (DO_V) lds_dma16(vb + off, &sm.v[r0][0]);
     }
 }
 
@@ -123,8 +128,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     constexpr int kBM = 32 * W;
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
     constexpr int DH = D / 2;    // head-dim values each half-wave supplies per query
+    // One-wave workgroups (short causal rows without a mask) stage K and V in ONE buffer,
+    // loaded out of phase: K(t + 1) streams in while the wave computes softmax(t) and P V(t),
+    // V(t + 1) while it computes Q K(t + 1).  16 KB of LDS per wave at D = 64 and no barriers:
+    // ten independent waves per CU, dispatched longest first.  (Two-wave workgroups couple
+    // their SIMDs through each tile's barrier, which left the long query tiles of such problems
+    // sharing their SIMDs for most of the kernel: B64 H6 L256 D64 47.0 -> 43.1 us.)
+    constexpr bool ONEBUF = ASYNC && W == 1 && !MASK && !SPLIT;
+    constexpr int NLD = kTileLoads<D, BN, W>;
     using Smem = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, FwdSmem<D, BN>>::type;
-    using Smem2 = typename std::conditional<ASYNC, FwdSmemAsync<D, BN>, NoSmem>::type;
+    using Smem2 = typename std::conditional<ASYNC && !ONEBUF, FwdSmemAsync<D, BN>, NoSmem>::type;
     __shared__ Smem sm;
     __shared__ Smem2 sm2;  // the second buffer of the asynchronous path
 
@@ -208,7 +221,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     const int t_end = SPLIT ? (piece + 1) * ntiles / npieces : ntiles;
 
     KVStage<D, BN, W> stage;
-    if constexpr (ASYNC) {
+    if constexpr (ONEBUF) {
+        if (t_begin < t_end) {
+            issue_tile<D, BN, W, true, false>(sm, kb, vb, t_begin * BN, s.S, wave, lane);
+            issue_tile<D, BN, W, false, true>(sm, kb, vb, t_begin * BN, s.S, wave, lane);
+        }
+    } else if constexpr (ASYNC) {
         if (t_begin < t_end) issue_tile<D, BN, W>(sm, kb, vb, t_begin * BN, s.S, wave, lane);
     } else if (s.vec && t_begin < t_end) {
         stage.load(kb, vb, t_begin * BN, s.S, tid);
@@ -220,7 +238,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
     // tn: the tile to stream in next (t + 1; -1: none).
     auto tile = [&](int t, auto &cur, auto &nxt, int tn) {
         const int n0 = t * BN;
-        if constexpr (ASYNC) {
+        if constexpr (ONEBUF) {
+            // In flight: K(t), then V(t).  (Every tile of a one-buffer wave has visible keys:
+            // causal tiles end at the wave's last query, so no tile takes the early return.)
+            wait_vmem_but<NLD>();
+        } else if constexpr (ASYNC) {
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile t landed
             __syncthreads();  // everyone's loads landed; everyone is done with the previous tile
             if (tn >= 0) issue_tile<D, BN, W>(nxt, kb, vb, tn * BN, s.S, wave, lane);
@@ -318,6 +340,27 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
             }
         }
 
+        if constexpr (ONEBUF) {
+            wait_lds();  // K(t)'s reads have returned: the buffer takes K(t + 1)
+            if (tn >= 0) issue_tile<D, BN, W, true, false>(sm, kb, vb, tn * BN, s.S, wave, lane);
+            // In flight: V(t), then K(t + 1).
+            if (tn >= 0) wait_vmem_but<NLD>();
+            else wait_vmem();
+        }
+        // With two or more waves the V operands are read ahead here (their LDS latency hides
+        // under the softmax) and each P column feeds its products as soon as it is formed:
+        // B8 H12 L1024 causal 131.4 -> 129.8 us, B1 H8 L2048 62.0 -> 60.1 us.  (One-wave
+        // workgroups measured faster without: 43.1 against 43.9 us.)
+        constexpr bool VAHEAD = D <= 64 && !ONEBUF;
+        float vv[VAHEAD ? NT : 1][VAHEAD ? D / 32 : 1][16];
+        if constexpr (VAHEAD) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) vv[kt][dt][r] = vread(kt * 32 + acc_row(r, g), dt * 32 + lr);
+        }
         // Scores in log2 units (masked on edge tiles); tile max per query.
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
@@ -359,6 +402,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
         }
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float ls = 0.f;
+        if constexpr (VAHEAD) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = exp2_fast(sacc[kt][r] - m_use);
+                    ls += p;
+                    if (live[kt]) {
+#pragma unroll
+                        for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = mfma_f32(vv[kt][dt][r], p, oacc[dt]);
+                    }
+                }
+            l_run += xor32_add(ls);
+            return;
+        }
 #pragma unroll
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
@@ -381,7 +439,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
                                         oacc[dt]);
         }
     };
-    if constexpr (ASYNC) {
+    if constexpr (ONEBUF) {
+        wait_vmem();  // the queries (and tile t_begin): no load of the loop waits for them again
+        for (int t = t_begin; t < t_end; ++t) {
+            const int tn = t + 1 < t_end ? t + 1 : -1;
+            tile(t, sm, sm, tn);
+            wait_lds();  // V(t)'s reads have returned: the buffer takes V(t + 1)
+            if (tn >= 0) issue_tile<D, BN, W, false, true>(sm, kb, vb, tn * BN, s.S, wave, lane);
+        }
+    } else if constexpr (ASYNC) {
         for (int t = t_begin; t < t_end; t += 2) {
             tile(t, sm, sm2, t + 1 < t_end ? t + 1 : -1);
             if (t + 1 < t_end) tile(t + 1, sm2, sm, t + 2 < t_end ? t + 2 : -1);
@@ -539,7 +605,11 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
                           32 * W, BN);
         }
     }
-    if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
+    if constexpr (W == 1) {  // short causal rows without a mask (with_config)
+        if (a.s.vec)
+            return launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a);
+        return launch(fwd_f32_kernel<D, BN, W, true, false, false>, grid, block, st, a);
+    } else if (a.s.vec && !(mask && a.s.causal)) {  // (causal + mask: register staging, fewer VGPRs)
         if (a.s.causal)
             return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true>, grid, block, st, a));
         else if (mask && a.s.msl == 0 && BN <= 64) {
@@ -575,16 +645,25 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
 }
 
 // The instantiation the forward runs for a shape: head dim D, key tile BN, waves W.  Short causal
-// problems take 2-wave workgroups over 32-key tiles: their causal work units are finer, which
-// balances the CUs better (measured on one MI355X: B64 H6 L256 D64 causal 54.0 -> 49.5 us; B8
-// H12 L1024 unchanged; non-causal B16 H16 L512 slower, 161 -> 171 us).  At D = 64 the 4-wave
-// workgroups take 32-key tiles: half the LDS of 64-key tiles (32 KB), so four workgroups fit a
-// CU instead of two (B8 H12 L1024 causal 148.7 -> 145.7 us, B2 H12 L4096 causal 480 -> 457 us).
+// problems take smaller workgroups over 32-key tiles: their causal work units are finer, which
+// balances the CUs better (measured on one MI355X: B64 H6 L256 D64 causal 54.0 -> 49.5 us with
+// 2 waves; B8 H12 L1024 unchanged; non-causal B16 H16 L512 slower, 161 -> 171 us), and one wave
+// each when no mask is given (49.5 -> 43.1 us, the one-buffer path of fwd_f32_kernel).  At D = 64
+// the 4-wave workgroups take 32-key tiles: half the LDS of 64-key tiles (32 KB), so four
+// workgroups fit a CU instead of two (B8 H12 L1024 causal 148.7 -> 145.7 us, B2 H12 L4096 causal
+// 480 -> 457 us).
 template <typename F>
 auto with_config(const AttnShape &s, F f) {
     const bool small = s.causal && s.L <= 256;
-    if (s.E <= 32) return small ? f.template operator()<32, 32, 2>() : f.template operator()<32, 64, 4>();
-    if (s.E <= 64) return small ? f.template operator()<64, 32, 2>() : f.template operator()<64, 32, 4>();
+    const bool one = small && s.mask == nullptr;
+    if (s.E <= 32) {
+        if (one) return f.template operator()<32, 32, 1>();
+        return small ? f.template operator()<32, 32, 2>() : f.template operator()<32, 64, 4>();
+    }
+    if (s.E <= 64) {
+        if (one) return f.template operator()<64, 32, 1>();
+        return small ? f.template operator()<64, 32, 2>() : f.template operator()<64, 32, 4>();
+    }
     return f.template operator()<128, 32, 4>();
 }
 
