@@ -66,18 +66,16 @@ struct QStage {
     f32x4 q[N], o[N];
     float lse, dsum;
 
+    // Rows past L read row L - 1 instead of zeros (no zero fill and no branch per step): their
+    // lse is +inf, so P = 0, dS = 0 and the finite values contribute nothing to dV, dK and the
+    // unwritten dQ rows.
     DEVI void load(const float *qb, const float *gb, const float *lseb, const float *dsumb, int m0,
                    int L, int tid) {
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4, qq = m0 + r;
-            if (qq < L) {
-                q[j] = *reinterpret_cast<const f32x4 *>(qb + (int64_t)qq * D + c);
-                o[j] = *reinterpret_cast<const f32x4 *>(gb + (int64_t)qq * D + c);
-            } else {
-                q[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-                o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4, qq = min(m0 + r, L - 1);
+            q[j] = *reinterpret_cast<const f32x4 *>(qb + (int64_t)qq * D + c);
+            o[j] = *reinterpret_cast<const f32x4 *>(gb + (int64_t)qq * D + c);
         }
         if (tid < kBM) {
             const int qq = m0 + tid;
@@ -357,10 +355,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
             if (t4 % 8 == 4) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
         }
 
-        // P and dS, elementwise in the accumulator layout; dS goes to the shared tile.  Keys
-        // past the end or (causal) past a query only occur when the wave's keys reach the end
-        // of the sequence or cross the diagonal of this query tile.
-        const bool edge = kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > m0);
+        // P and dS, elementwise in the accumulator layout; dS goes to the shared tile.
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int qrow = acc_row(r, g), qq = m0 + qrow;
@@ -368,10 +363,22 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
             // then one conversion to base 2 for v_exp_f32.
             float x = sacc[r] * s.scale;
             if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
-            float p = exp2_fast((x - sm.lse[qrow]) * kLog2e);
-            if (edge && (key >= s.S || (CAUSAL && key > qq))) p = 0.f;
-            sacc[r] = p;
-            pacc[r] = p * (pacc[r] - sm.dsum[qrow]);
+            sacc[r] = exp2_fast((x - sm.lse[qrow]) * kLog2e);
+        }
+        // Keys past the end or (causal) past a query only occur when the wave's keys reach the
+        // end of the sequence or cross the diagonal of this query tile: a wave-uniform branch,
+        // so the other steps spend no VALU on the test (float32 MFMAs and VALU instructions do
+        // not overlap on a SIMD).
+        if (kw0 + 31 >= s.S || (CAUSAL && kw0 + 31 > m0)) {
+            asm volatile("" ::: "memory");  // keeps the branch: not if-converted into selects
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (key >= s.S || (CAUSAL && key > m0 + acc_row(r, g))) sacc[r] = 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int qrow = acc_row(r, g);
+            pacc[r] = sacc[r] * (pacc[r] - sm.dsum[qrow]);
             sm.ds[qrow][wave * 32 + lr] = pacc[r];
         }
 
