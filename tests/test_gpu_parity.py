@@ -188,6 +188,7 @@ def test_attention_rank4(oracle_lib, mode):
     (2, 4, 2, 5, 5, 8, True),        # tests/test_torch_api_f1.py:78-84
     (1, 6, 2, 300, 300, 64, True),
     (2, 8, 1, 130, 250, 32, False),
+    (1, 4, 2, 200, 200, 32, True),   # short causal rows: one-wave forward, D = 32
 ])
 def test_grouped_heads(oracle_lib, B, H, Hkv, L, S, E, causal):
     rng = np.random.default_rng(B * 1000 + H * 10 + Hkv)
@@ -201,6 +202,9 @@ def test_grouped_heads(oracle_lib, B, H, Hkv, L, S, E, causal):
     (2, 2, 257, 191, 64, True), (1, 3, 191, 257, 64, False), (1, 2, 130, 70, 128, True),
     (1, 2, 65, 300, 128, False), (1, 1, 40, 40, 100, True), (1, 1, 33, 47, 1, False),
     (1, 1, 50, 60, 31, True), (3, 1, 200, 200, 64, True),
+    # short causal rows (L <= 256, no mask) take the one-wave forward: aligned D = 32 and 64, keys
+    # beyond the queries, a ragged last tile
+    (2, 3, 100, 100, 32, True), (1, 2, 96, 160, 64, True), (2, 1, 256, 256, 32, True),
 ])
 def test_tile_edges(oracle_lib, B, H, L, S, E, causal):
     rng = np.random.default_rng(B + 7 * H + 13 * L + 17 * S + 19 * E)
