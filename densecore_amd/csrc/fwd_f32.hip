@@ -192,6 +192,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
             }
         }
     }
+    // Without a mask the scale is applied after the tile max and inside each exponent's FMA
+    // (float32 MFMAs and VALU instructions do not overlap, and this saves a multiply per score):
+    // for a positive scale the max of the rounded products equals the rounded product of the
+    // max, so the running max is unchanged, and the exponent is rounded once instead of twice.
+    // A negative scale enters as its magnitude with the queries negated; a zero scale as the
+    // smallest normal float (every visible score then gives exp2 of a value below 2^-100, which
+    // is 1, as it is with 0).
+    const float csc = MASK ? 0.f : fmaxf(fabsf(s.scale_log2), 0x1p-126f);
+    if (!MASK && s.scale_log2 < 0.f) {
+#pragma unroll
+        for (int t = 0; t < DH; ++t) qreg[t] = -qreg[t];
+    }
     const float *mrow = nullptr;
     if (MASK) mrow = s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh + (int64_t)qi * s.msl;
     // ROWMASK: the mask does not depend on the query (stride 0 along L, e.g. key padding).  Each
@@ -361,17 +373,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
 #pragma unroll
                     for (int r = 0; r < 16; ++r) vv[kt][dt][r] = vread(kt * 32 + acc_row(r, g), dt * 32 + lr);
         }
-        // Scores in log2 units (masked on edge tiles); tile max per query.
+        // Scores in log2 units (with a mask; without one the raw products, see csc), masked on
+        // edge tiles; tile max per query.
+        if constexpr (MASK) {
 #pragma unroll
-        for (int kt = 0; kt < NT; ++kt)
+            for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if constexpr (MASK) {
-                    sacc[kt][r] = (sacc[kt][r] * s.scale + mv[kt][r]) * kLog2e;
-                } else {
-                    sacc[kt][r] *= s.scale_log2;
-                }
-            }
+                for (int r = 0; r < 16; ++r) sacc[kt][r] = (sacc[kt][r] * s.scale + mv[kt][r]) * kLog2e;
+        }
         if (edge) {
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt)
@@ -387,6 +396,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
         mx = xor32_max(mx);
+        if constexpr (!MASK) mx *= csc;
+        // p = 2^(score in log2 units - m)
+        auto expo = [&](float x, float m) { return exp2_fast(MASK ? x - m : fmaf(x, csc, -m)); };
         // Lazy rescaling: the exponent reference m_run moves (and O, l are rescaled) only when
         // some lane's tile max exceeds it by more than 8, so P <= 2^8 and most tiles skip the
         // rescale of the accumulator; out = O / l and lse = m_run + log2(l) are unchanged.
@@ -407,7 +419,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
             for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float p = exp2_fast(sacc[kt][r] - m_use);
+                    const float p = expo(sacc[kt][r], m_use);
                     ls += p;
                     if (live[kt]) {
 #pragma unroll
@@ -421,7 +433,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
         for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = exp2_fast(sacc[kt][r] - m_use);
+                const float p = expo(sacc[kt][r], m_use);
                 sacc[kt][r] = p;
                 ls += p;
             }

@@ -197,6 +197,40 @@ def test_grouped_heads(oracle_lib, B, H, Hkv, L, S, E, causal):
     _check(oracle_lib, q, k, v, g, causal, tag="gqa")
 
 
+@pytest.mark.parametrize("scale", [-0.4, 0.0])
+@pytest.mark.parametrize("B,H,L,S,E,causal", [
+    (2, 2, 100, 100, 64, True),   # one-wave forward
+    (1, 3, 300, 300, 64, True),   # 4-wave forward
+    (1, 2, 600, 600, 64, True),   # split key ranges
+    (1, 2, 200, 300, 32, False),  # 64-key tiles
+])
+def test_negative_and_zero_scale(oracle_lib, B, H, L, S, E, causal, scale):
+    """A scale passed explicitly may be negative or zero (the reference takes any float): without
+    a mask the forward applies the scale after the tile max, with negated queries for a negative
+    one, and treats zero as the smallest normal float.  Causal rows are checked against the
+    oracle without causal masking and with the equivalent additive mask: the reference writes
+    -inf into masked scores before scaling them, so a negative or zero scale makes its causal rows
+    NaN (-inf times -0.4 is +inf, times 0 is NaN), while here, as in PyTorch, masked keys get
+    probability 0 whatever the scale."""
+    rng = np.random.default_rng(B + 3 * H + 5 * L + 7 * S + 11 * E)
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, H, S, E), dtype=np.float32) for _ in range(2))
+    if not causal:
+        _check(oracle_lib, q, k, v, g, False, scale, tag=f"scale {scale}")
+        return
+    print(f"[case] causal scale {scale} q{q.shape}", flush=True)
+    tri = np.where(np.arange(S)[None, :] <= np.arange(L)[:, None], 0.0, -np.inf).astype(np.float32)
+    full = np.ascontiguousarray(np.broadcast_to(tri, (B, H, L, S)))
+    ref_o, ref_l = oracle_lib.forward(q, k, v, False, scale, full)
+    out, lse = _run_fwd(q, k, v, True, scale, None)
+    assert_f32(out, ref_o, f"causal scale {scale} out")
+    assert_f32(lse, ref_l, f"causal scale {scale} lse")
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, False, scale, full)
+    got = _run_bwd(g, q, k, v, ref_o, ref_l, True, scale, None)
+    for name, x, y in zip(("dq", "dk", "dv"), got, ref):
+        assert_f32(x, y, f"causal scale {scale} {name}")
+
+
 @pytest.mark.parametrize("B,H,L,S,E,causal", [
     (1, 1, 1, 1, 64, False), (1, 2, 1, 700, 64, False), (1, 1, 129, 1, 64, True),
     (2, 2, 257, 191, 64, True), (1, 3, 191, 257, 64, False), (1, 2, 130, 70, 128, True),
