@@ -75,9 +75,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
 
     // Scores are formed as fma(q.k, c, -m) in base-2 units; a negative scale is folded into
-    // the queries (a sign flip, exact) so that the max of the raw products is the max score.
+    // the queries (a sign flip, exact) so that the max of the raw products is the max score.  A
+    // zero scale enters as the smallest normal float: every visible key then gets P = 1, as with
+    // 0, and a masked (-inf) score stays -inf instead of becoming -inf * 0 = NaN.
     const bool neg = s.scale_log2 < 0.f;
-    const float c = MASK ? 1.f : (neg ? -s.scale_log2 : s.scale_log2);
+    const float c = MASK ? 1.f : fmaxf(fabsf(s.scale_log2), 0x1p-126f);
 
     // Queries: step t, half g supplies Q[qi][16t + 8g + 0..7].
     bf16x8 qreg[KSTEP];
@@ -314,8 +316,8 @@ __global__ __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     const __bf16 *kb = static_cast<const __bf16 *>(a.k) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
     const __bf16 *vb = static_cast<const __bf16 *>(a.v) + (int64_t)(b * s.Hkv + hk) * s.S * s.E;
 
-    const bool neg = s.scale_log2 < 0.f;
-    const float c = neg ? -s.scale_log2 : s.scale_log2;
+    const bool neg = s.scale_log2 < 0.f;  // folded as in fwd_bf16_kernel, zero scale included
+    const float c = fmaxf(fabsf(s.scale_log2), 0x1p-126f);
     bf16x8 qreg[KSTEP];
     {
         const __bf16 *qrow = static_cast<const __bf16 *>(a.q) + ((int64_t)bh * s.L + qi) * s.E;
