@@ -57,12 +57,15 @@ struct alignas(16) BwdSmem {
     float dsum[kBM];
 };
 
+// Threads of a backward workgroup: 4 waves of 32 keys, or at D = 128 8 waves of 16 keys.
+constexpr int bwd_threads(int D) { return D == 128 ? 2 * kThreads : kThreads; }
+
 // Register staging of one step's Q and dO rows (fast path: E == D, 16-byte aligned).
-template <int D>
+template <int D, int NT = bwd_threads(D)>
 struct QStage {
     static constexpr int C4 = D / 4;
-    static constexpr int N = kBM * C4 / kThreads;
-    static_assert(kBM * C4 % kThreads == 0, "tile must split evenly over the workgroup");
+    static constexpr int N = kBM * C4 / NT;
+    static_assert(kBM * C4 % NT == 0, "tile must split evenly over the workgroup");
     f32x4 q[N], o[N];
     float lse, dsum;
 
@@ -73,7 +76,7 @@ struct QStage {
                    int L, int tid) {
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4, qq = min(m0 + r, L - 1);
+            const int i = tid + NT * j, r = i / C4, c = (i % C4) * 4, qq = min(m0 + r, L - 1);
             q[j] = *reinterpret_cast<const f32x4 *>(qb + (int64_t)qq * D + c);
             o[j] = *reinterpret_cast<const f32x4 *>(gb + (int64_t)qq * D + c);
         }
@@ -86,7 +89,7 @@ struct QStage {
     DEVI void store(BwdSmem<D> &sm, int tid) const {
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-            const int i = tid + kThreads * j, r = i / C4, c = (i % C4) * 4;
+            const int i = tid + NT * j, r = i / C4, c = (i % C4) * 4;
             *reinterpret_cast<f32x4 *>(&sm.q[r][c]) = q[j];
             *reinterpret_cast<f32x4 *>(&sm.dout[r][c]) = o[j];
         }
@@ -98,7 +101,7 @@ struct QStage {
 template <int D>
 DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const float *lseb,
                         const float *dsumb, int m0, int L, int E, int tid) {
-    for (int i = tid; i < kBM * D; i += kThreads) {
+    for (int i = tid; i < kBM * D; i += bwd_threads(D)) {
         const int r = i / D, c = i % D, qq = m0 + r;
         const bool ok = qq < L && c < E;
         sm.q[r][c] = ok ? qb[(int64_t)qq * E + c] : 0.f;
@@ -115,7 +118,8 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
 // m0 .. m0 + 31.  `dst` points at row m0 of the destination (row stride E); rows at or past
 // `nrows` are not written.  ATOMIC adds scale * dS K into the float32 dq with float atomics;
 // otherwise dS K is stored (the reduction applies the scale) into the tile's own dQ slot.  The
-// 32 x D tile is split into 16 x 16 blocks, D/32 per wave (v_mfma_f32_16x16x4_f32: lane l supplies
+// 32 x D tile is split into 16 x 16 blocks, D/32 per wave of 4 (D/64 per wave of 8)
+// (v_mfma_f32_16x16x4_f32: lane l supplies
 // A[l%16][l/16] and B[l/16][l%16] and holds C[4*(l/16) + v][l%16]), so each element is written
 // exactly once per workgroup step.  The reduction index is permuted so that a lane's four
 // steps over a 16-key block take four consecutive keys: step u of block kb gives lane l key
@@ -125,10 +129,11 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
 template <int D>
 DEVI void dq_product(const BwdSmem<D> &sm, float *dst, bool atomic, int nrows, int nkeys, int E,
                      float scale, int wave, int lane) {
-    constexpr int TPW = D / 32;
+    constexpr int WH = bwd_threads(D) / 128;  // waves per 16-query half (the D dims split WH ways)
+    constexpr int TPW = D / (16 * WH);
     constexpr int NB = kBN / 16;  // 16-key blocks in a full tile
     const int r16 = lane & 15, c4 = lane >> 4;
-    const int qh = wave >> 1, dbase = (wave & 1) * (D / 2);
+    const int qh = wave / WH, dbase = (wave % WH) * (D / WH);
     const float *arow = &sm.ds[qh * 16 + r16][4 * c4];
     const float *brow = &sm.kt[dbase + r16][4 * c4];
     constexpr int BSTRIDE = 16 * (kBN + 4);  // words between the wave's 16 x 16 output blocks
@@ -454,14 +459,278 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     }
 }
 
+// key_tile at D = 128: 8 waves of 16 keys (v_mfma_f32_16x16x4_f32), two waves per SIMD.  With 32
+// keys per wave (key_tile) the dK^T, dV^T accumulators and the V row take ~290 registers of a
+// wave, so that kernel runs one wave per SIMD; here each wave holds 2 x 32 accumulator registers
+// and its keys' V rows in 32 (K comes from the workgroup's transposed K tile in LDS, which the dQ
+// product reads anyway).  Same steps, same shared tiles (the 8 waves fill a 128-key tile), same
+// dQ product (16 x 16 blocks, two per wave) and stores.  The products:
+//   * S and dP with queries as rows, in two 16-query halves: the reduction over d runs in 16-dim
+//     blocks whose step u gives lane l dim 16 j + 4 (l / 16) + u, so a lane's Q and dO operands
+//     for a block are one ds_read_b128 each, its V operands registers and its K operands four
+//     ds_read_b32 of the K^T tile (rows 4 apart: the four lane groups hit banks 16 apart);
+//   * the accumulators hold S[16 qh + 4 (l / 16) + v][key l % 16] (v = 0..3), which are the
+//     B operands of dV^T += dO^T P and dK^T += Q^T dS with the reduction over queries taken in
+//     the order (qh, v, l / 16): the lane's P and dS values enter as they are.
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
+DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
+                     float *vdst, bool kv_atomic) {
+    static_assert(D == 128, "the 8-wave tile is for head dim 128");
+    constexpr int NT = bwd_threads(D), NKB = D / 16;
+
+    const AttnShape &s = a.s;
+    const int wave = tid >> 6, lane = tid & 63, r16 = lane & 15, c4 = lane >> 4;
+    const int b = bhk / s.Hkv, hk = bhk % s.Hkv;
+    const int n0 = kt * kBN;
+    const int kw0 = n0 + wave * 16;  // this wave's first key
+    const int key = kw0 + r16;       // this lane's key column
+
+    const float *kb = static_cast<const float *>(a.k) + (int64_t)bhk * s.S * s.E;
+    const float *vb = static_cast<const float *>(a.v) + (int64_t)bhk * s.S * s.E;
+
+    // V of this lane's key at dims 16 j + 4 c4 + 0..3.
+    f32x4 vreg[NKB];
+#pragma unroll
+    for (int j = 0; j < NKB; ++j) {
+        const int d = 16 * j + 4 * c4;
+        if (VEC && key < s.S) {
+            vreg[j] = *reinterpret_cast<const f32x4 *>(vb + (int64_t)key * D + d);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vreg[j][u] = (key < s.S && d + u < s.E) ? vb[(int64_t)key * s.E + d + u] : 0.f;
+        }
+    }
+    // The workgroup's K tile, transposed into LDS for the dQ product.
+    if (VEC) {
+        for (int i = tid; i < kBN * (D / 4); i += NT) {
+            const int r = i % kBN, c = (i / kBN) * 4, kk = n0 + r;
+            const f32x4 x = kk < s.S ? *reinterpret_cast<const f32x4 *>(kb + (int64_t)kk * D + c)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sm.kt[c + u][r] = x[u];
+        }
+    } else {
+        for (int i = tid; i < kBN * D; i += NT) {
+            const int r = i % kBN, c = i / kBN, kk = n0 + r;
+            sm.kt[c][r] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
+        }
+    }
+
+    // dV^T and dK^T: block j holds dims 16 j + 4 c4 + v (v = 0..3) of this lane's key.
+    f32x4 dk[NKB], dv[NKB];
+#pragma unroll
+    for (int j = 0; j < NKB; ++j) dk[j] = f32x4{0.f, 0.f, 0.f, 0.f}, dv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int m_begin = tile_m_begin(CAUSAL, kt);
+    const int per_head = tile_per_head(s, kt);
+    const int key_end = min(kBN, s.S - n0);  // keys of this tile that exist
+    auto step_head = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
+    auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kBM; };
+    auto step_keys = [&](int m0) { return CAUSAL ? max(0, min(key_end, m0 + kBM - n0)) : key_end; };
+    const bool dq_atomic = a.dq_part == nullptr;
+    const int rf = slot_from(s, kt);
+    const int64_t slot0 = slot_before(s, kt) * ((int64_t)s.B * s.H);
+    auto dq_dst = [&](int bh, int m0) -> float * {
+        if (dq_atomic) return a.dq_acc + ((int64_t)bh * s.L + m0) * s.E;
+        return a.dq_part + (slot0 + (int64_t)bh * (s.L - rf) + (m0 - rf)) * s.E;
+    };
+
+    QStage<D> stage;
+    if (VEC && i0 < i1) {
+        const int bh = step_head(i0);
+        stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
+                   static_cast<const float *>(a.dout) + (int64_t)bh * s.L * D,
+                   a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, step_m0(i0), s.L, tid);
+    }
+    int prev_bh = -1, prev_m0 = 0;
+    for (int i = i0; i < i1; ++i) {
+        const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
+        __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
+        if (prev_bh >= 0)
+            dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
+                          s.scale, wave, lane);
+        if (VEC) {
+            stage.store(sm, tid);
+        } else {
+            stage_generic<D>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
+                             static_cast<const float *>(a.dout) + (int64_t)bh * s.L * s.E,
+                             a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
+        }
+        __syncthreads();  // the tile is staged and the previous dQ product has read sm.ds
+        if (VEC && i + 1 < i1) {
+            const int nbh = step_head(i + 1);
+            stage.load(static_cast<const float *>(a.q) + (int64_t)nbh * s.L * D,
+                       static_cast<const float *>(a.dout) + (int64_t)nbh * s.L * D,
+                       a.lse + (int64_t)nbh * s.L, a.dsum + (int64_t)nbh * s.L, step_m0(i + 1),
+                       s.L, tid);
+        }
+        prev_bh = bh, prev_m0 = m0;
+
+        const bool live = kw0 < s.S && (!CAUSAL || m0 + kBM - 1 >= kw0);
+        if (!live) continue;
+        const float *mbase = MASK ? s.mask + (int64_t)b * s.msb + (int64_t)h * s.msh : nullptr;
+
+        // S = Q K^T and dP = dO V^T for the two 16-query halves.  Each 16-dim block's Q and dO
+        // operands are read while the previous block's MFMAs run (two buffers; left to itself the
+        // compiler reads all of them up front and runs out of registers).
+        f32x4 sacc[2], pacc[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) sacc[qh] = f32x4{0.f, 0.f, 0.f, 0.f}, pacc[qh] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 qop[2][2], oop[2][2], kop[2];  // [buffer][query half]; K: [buffer]
+        auto read_qo = [&](int j, int buf) {
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                qop[buf][qh] = *reinterpret_cast<const f32x4 *>(&sm.q[16 * qh + r16][16 * j + 4 * c4]);
+                oop[buf][qh] = *reinterpret_cast<const f32x4 *>(&sm.dout[16 * qh + r16][16 * j + 4 * c4]);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kop[buf][u] = sm.kt[16 * j + 4 * c4 + u][wave * 16 + r16];
+        };
+        read_qo(0, 0);
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+            if (j + 1 < NKB) read_qo(j + 1, (j + 1) & 1);
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    sacc[qh] = __builtin_amdgcn_mfma_f32_16x16x4f32(qop[j & 1][qh][u], kop[j & 1][u], sacc[qh], 0, 0, 0);
+                    pacc[qh] = __builtin_amdgcn_mfma_f32_16x16x4f32(oop[j & 1][qh][u], vreg[j][u], pacc[qh], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // P and dS, elementwise in the accumulator layout (rows 16 qh + 4 c4 + v); dS goes to the
+        // shared tile.  scale * q.k (+ mask) - lse in natural-log units, then one conversion to
+        // base 2, as in key_tile.
+        f32x4 dsum4[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&sm.lse[16 * qh + 4 * c4]);
+            dsum4[qh] = *reinterpret_cast<const f32x4 *>(&sm.dsum[16 * qh + 4 * c4]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int qq = m0 + 16 * qh + 4 * c4 + v;
+                float x = sacc[qh][v] * s.scale;
+                if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+                sacc[qh][v] = exp2_fast((x - l4[v]) * kLog2e);
+            }
+        }
+        // Keys past the end or (causal) past a query only occur on the edge steps: a
+        // wave-uniform branch (see key_tile).
+        if (kw0 + 15 >= s.S || (CAUSAL && kw0 + 15 > m0)) {
+            asm volatile("" ::: "memory");  // keeps the branch: not if-converted into selects
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (key >= s.S || (CAUSAL && key > m0 + 16 * qh + 4 * c4 + v)) sacc[qh][v] = 0.f;
+        }
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                pacc[qh][v] = sacc[qh][v] * (pacc[qh][v] - dsum4[qh][v]);
+                sm.ds[16 * qh + 4 * c4 + v][wave * 16 + r16] = pacc[qh][v];
+            }
+
+        // dV^T += dO^T P and dK^T += Q^T dS: step (qh, v) reduces over queries 16 qh + 4 (l/16) + v.
+        // The dO^T and Q^T operands of a 16-dim block are read during the previous block's MFMAs.
+        float top[2][2][8];  // [buffer][dO, Q][qh * 4 + v]
+        auto read_t = [&](int j, int buf) {
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int qrow = 16 * qh + 4 * c4 + v;
+                    top[buf][0][4 * qh + v] = sm.dout[qrow][16 * j + r16];
+                    top[buf][1][4 * qh + v] = sm.q[qrow][16 * j + r16];
+                }
+        };
+        read_t(0, 0);
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+            if (j + 1 < NKB) read_t(j + 1, (j + 1) & 1);
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    dv[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(top[j & 1][0][4 * qh + v], sacc[qh][v], dv[j], 0, 0, 0);
+                    dk[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(top[j & 1][1][4 * qh + v], pacc[qh][v], dk[j], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __syncthreads();
+    if (prev_bh >= 0)
+        dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
+                      wave, lane);
+
+    if (kv_atomic) {
+        // As in key_tile: each wave's 16 x D block goes through LDS, then one atomic per element
+        // along consecutive dims of one key.
+        constexpr int RS = D + 4;
+        static_assert(8 * 16 * RS * sizeof(float) <= sizeof(BwdSmem<D>), "per-wave blocks fit");
+        float *blk = reinterpret_cast<float *>(&sm) + wave * 16 * RS;
+        const int rows = min(16, s.S - kw0);
+        auto flush = [&](const f32x4 (&acc)[NKB], float mul, float *dst) {
+            __syncthreads();  // the previous readers of the area are done
+#pragma unroll
+            for (int j = 0; j < NKB; ++j)
+                *reinterpret_cast<f32x4 *>(blk + r16 * RS + 16 * j + 4 * c4) =
+                    f32x4{acc[j][0] * mul, acc[j][1] * mul, acc[j][2] * mul, acc[j][3] * mul};
+            __syncthreads();
+            for (int i = lane; i < rows * D; i += 64) {
+                const int rr = i / D, d = i % D;
+                if (d < s.E) unsafeAtomicAdd(dst + (int64_t)rr * s.E + d, blk[rr * RS + d]);
+            }
+        };
+        flush(dk, s.scale, kdst + (int64_t)(kw0 - n0) * s.E);
+        flush(dv, 1.f, vdst + (int64_t)(kw0 - n0) * s.E);
+        return;
+    }
+
+    // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
+    if (key < s.S) {
+        float *dkr = kdst + (int64_t)(key - n0) * s.E;
+        float *dvr = vdst + (int64_t)(key - n0) * s.E;
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+            const int d = 16 * j + 4 * c4;
+            if (VEC) {
+                *reinterpret_cast<f32x4 *>(dkr + d) =
+                    f32x4{dk[j][0] * s.scale, dk[j][1] * s.scale, dk[j][2] * s.scale, dk[j][3] * s.scale};
+                *reinterpret_cast<f32x4 *>(dvr + d) = dv[j];
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (d + u < s.E) {
+                        dkr[d + u] = dk[j][u] * s.scale;
+                        dvr[d + u] = dv[j][u];
+                    }
+            }
+        }
+    }
+}
+
+// The key tile of either layout.
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+DEVI void key_tile_any(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
+                       float *vdst, bool kv_atomic) {
+    if constexpr (D == 128)
+        key_tile16<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
+    else
+        key_tile<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
+}
+
+template <int D, bool CAUSAL, bool MASK, bool VEC>
+__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(D == 128 || (D <= 64 && !MASK) ? 2 : 1, D == 128 || (D <= 64 && !MASK) ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
     __shared__ BwdSmem<D> sm;
     const int BHk = a.s.B * a.s.Hkv;
     const int kt = blockIdx.x / BHk;  // tile 0 has the most causal work, so it goes first
     const int bhk = blockIdx.x % BHk;
     const int64_t row0 = ((int64_t)bhk * a.s.S + (int64_t)kt * kBN) * a.s.E;
-    key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, 0, tile_steps(a.s, kt),
+    key_tile_any<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, 0, tile_steps(a.s, kt),
                                    static_cast<float *>(a.dk) + row0, static_cast<float *>(a.dv) + row0, false);
 }
 
@@ -476,7 +745,7 @@ DEVI float *kv_slot(const BwdArgs &a, int64_t range, int which) {
 // blocks (workgroup w runs on XCD w % 8), so the key tiles of one kv head, which read the same
 // Q / dO, share an L2.
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 64 && !MASK ? 2 : 1, D <= 64 && !MASK ? 2 : 1))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
+__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(D == 128 || (D <= 64 && !MASK) ? 2 : 1, D == 128 || (D <= 64 && !MASK) ? 2 : 1))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
     __shared__ BwdSmem<D> sm;
     const int w = blockIdx.x;
     const int64_t c = (int64_t)(w & 7) * (sk.chunks >> 3) + (w >> 3);
@@ -504,7 +773,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 6
             kd = kv_slot(a, c, first ? 0 : 1);
             vd = kd + (int64_t)kBN * a.s.E;
         }
-        key_tile<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, kd, vd, !whole && !a.kv_part);
+        key_tile_any<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, kd, vd, !whole && !a.kv_part);
         first = false;
         pos += i1 - i;
         i = 0;
@@ -675,14 +944,14 @@ template <int D, bool VEC>
 hipError_t launch_dv(const BwdArgs &a, const StreamK &sk, hipStream_t st) {
     const bool mask = a.s.mask != nullptr;
     if (sk.chunks > 0) {
-        const dim3 grid(sk.chunks), block(kThreads);
+        const dim3 grid(sk.chunks), block(bwd_threads(D));
         if (a.s.causal && mask) return launch(bwd_f32_streamk_kernel<D, true, true, VEC>, grid, block, st, a, sk);
         if (a.s.causal) return launch(bwd_f32_streamk_kernel<D, true, false, VEC>, grid, block, st, a, sk);
         if (mask) return launch(bwd_f32_streamk_kernel<D, false, true, VEC>, grid, block, st, a, sk);
         return launch(bwd_f32_streamk_kernel<D, false, false, VEC>, grid, block, st, a, sk);
     }
     const int nkt = (a.s.S + kBN - 1) / kBN;
-    const dim3 grid(nkt * a.s.B * a.s.Hkv), block(kThreads);
+    const dim3 grid(nkt * a.s.B * a.s.Hkv), block(bwd_threads(D));
     if (a.s.causal && mask) return launch(bwd_f32_kernel<D, true, true, VEC>, grid, block, st, a);
     if (a.s.causal) return launch(bwd_f32_kernel<D, true, false, VEC>, grid, block, st, a);
     if (mask) return launch(bwd_f32_kernel<D, false, true, VEC>, grid, block, st, a);
