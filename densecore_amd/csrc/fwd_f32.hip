@@ -123,7 +123,7 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
 }
 
 template <int D, int BN, int W, bool CAUSAL, bool MASK, bool ASYNC, bool ROWMASK = false, bool SPLIT = false>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 || !ASYNC ? 2 : 1, D <= 64 || !ASYNC ? 2 : 1))) void fwd_f32_kernel(FwdArgs a) {
     [[maybe_unused]] constexpr int kThreads = 64 * W;
     constexpr int kBM = 32 * W;
     constexpr int NT = BN / 32;  // key sub-tiles of 32 per kv tile
@@ -579,11 +579,19 @@ __global__ __launch_bounds__(1024) void rowmask_batch_order_kernel(FwdArgs a, in
 }
 
 // The split of this instantiation's grid on the current device (fwd_split.hpp).
+// Split pieces at D = 128 take the register-staged kernel: it fits two waves per SIMD (the
+// asynchronous one needs ~330 registers for its swizzled LDS addresses and runs one), and few
+// long rows gain from that (B1 H8 L2048 D128 causal 125 -> 104 us) while full grids do not
+// (B2 H16 L2048 D128 causal 347 -> 396 us: those keep the asynchronous kernel).
+template <int D>
+constexpr bool kSplitAsync = D != 128;
+
 template <int D, int BN, int W>
 FwdSplitPlan plan(const AttnShape &s) {
     const int64_t blocks = (int64_t)(s.L + 32 * W - 1) / (32 * W) * s.B * s.H;
     const int64_t slots = split_slots(
-        reinterpret_cast<const void *>(&fwd_f32_kernel<D, BN, W, true, false, true, false, true>), 64 * W, blocks);
+        reinterpret_cast<const void *>(&fwd_f32_kernel<D, BN, W, true, false, kSplitAsync<D>, false, true>), 64 * W,
+        blocks);
     return plan_split(s, 32 * W, BN, slots);
 }
 
@@ -602,7 +610,7 @@ hipError_t launch_d(const FwdArgs &args, hipStream_t st) {
             a.split_chunk = p.chunk, a.split_max = p.max_pieces;
             a.split_lse = a.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
             const dim3 sgrid((unsigned)p.blocks);
-            if (a.s.vec) {
+            if (a.s.vec && kSplitAsync<D>) {
                 if (a.s.causal)
                     return_if(launch(fwd_f32_kernel<D, BN, W, true, false, true, false, true>, sgrid, block, st, a));
                 else
