@@ -581,8 +581,10 @@ __global__ __launch_bounds__(1024) void rowmask_batch_order_kernel(FwdArgs a, in
 // The split of this instantiation's grid on the current device (fwd_split.hpp).
 // Split pieces at D = 128 take the register-staged kernel: it fits two waves per SIMD (the
 // asynchronous one needs ~330 registers for its swizzled LDS addresses and runs one), and few
-// long rows gain from that (B1 H8 L2048 D128 causal 125 -> 104 us) while full grids do not
-// (B2 H16 L2048 D128 causal 347 -> 396 us: those keep the asynchronous kernel).
+// long rows gain from that (B1 H8 L2048 D128 causal: 111.8 -> 109.5 us in bench.py's schedule
+// timings, 125 -> 104 us over 200 back-to-back calls after 1000 warm-up calls) while full grids
+// lose (B2 H16 L2048 D128 causal 347 -> 396 us, same back-to-back timing): those keep the
+// asynchronous kernel.
 template <int D>
 constexpr bool kSplitAsync = D != 128;
 
