@@ -57,8 +57,13 @@ struct alignas(16) BwdSmem {
     float dsum[kBM];
 };
 
-// Threads of a backward workgroup: 4 waves of 32 keys, or at D = 128 8 waves of 16 keys.
-constexpr int bwd_threads(int D) { return D == 128 ? 2 * kThreads : kThreads; }
+// Threads of a backward workgroup: 8 waves of 16 keys at D = 128 (key_tile16), 4 waves of 32 keys
+// otherwise (key_tile).
+constexpr bool kSixteenKeys(int D) { return D == 128; }
+constexpr int bwd_threads(int D) { return kSixteenKeys(D) ? 2 * kThreads : kThreads; }
+// Waves per SIMD the kernels are built for: D = 128 two (one 8-wave workgroup per CU); below,
+// two without a mask (two 4-wave workgroups), one with.
+constexpr int bwd_waves_per_eu(int D, bool mask) { return D == 128 ? 2 : (mask ? 1 : 2); }
 
 // Register staging of one step's Q and dO rows (fast path: E == D, 16-byte aligned).
 template <int D, int NT = bwd_threads(D)>
@@ -461,10 +466,15 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
 
 // key_tile at D = 128: 8 waves of 16 keys (v_mfma_f32_16x16x4_f32), two waves per SIMD.  With 32
 // keys per wave (key_tile) the dK^T, dV^T accumulators and the V row take ~290 registers of a
-// wave, so that kernel runs one wave per SIMD; here each wave holds 2 x 32 accumulator registers
-// and its keys' V rows in 32 (K comes from the workgroup's transposed K tile in LDS, which the dQ
-// product reads anyway).  Same steps, same shared tiles (the 8 waves fill a 128-key tile), same
-// dQ product (16 x 16 blocks, two per wave) and stores.  The products:
+// wave, so that kernel ran one wave per SIMD; here each wave holds 2 x 32 accumulator registers
+// and its keys' V rows in 32 (K comes from the workgroup's transposed K tile in LDS, which the
+// dQ product reads anyway).  Same steps, same shared tiles (the 8 waves fill a 128-key tile),
+// same dQ product (16 x 16 blocks, two per wave) and stores.  One difference: key_tile forms S
+// with the forward's product and pairing of dims (v_mfma_f32_32x32x2_f32), so P = exp(S - lse)
+// normalizes to the forward's lse exactly; here S is rounded in another order, ~1e-5 relative
+// apart for scores near 100 (gradient errors up to ~5x the oracle's there; at ordinary scores
+// far below the bar).  The same layout at D = 64 measured 355 -> 343 us on B8 H12 L1024 but
+// keeps key_tile for that consistency.  The products:
 //   * S and dP with queries as rows, in two 16-query halves: the reduction over d runs in 16-dim
 //     blocks whose step u gives lane l dim 16 j + 4 (l / 16) + u, so a lane's Q and dO operands
 //     for a block are one ds_read_b128 each, its V operands registers and its K operands four
@@ -475,7 +485,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
 template <int D, bool CAUSAL, bool MASK, bool VEC>
 DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
                      float *vdst, bool kv_atomic) {
-    static_assert(D == 128, "the 8-wave tile is for head dim 128");
+    static_assert(kSixteenKeys(D), "the 8-wave tile is for head dim 128");
     constexpr int NT = bwd_threads(D), NKB = D / 16;
 
     const AttnShape &s = a.s;
@@ -717,14 +727,14 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
 template <int D, bool CAUSAL, bool MASK, bool VEC>
 DEVI void key_tile_any(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
                        float *vdst, bool kv_atomic) {
-    if constexpr (D == 128)
+    if constexpr (kSixteenKeys(D))
         key_tile16<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
     else
         key_tile<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
 }
 
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(D == 128 || (D <= 64 && !MASK) ? 2 : 1, D == 128 || (D <= 64 && !MASK) ? 2 : 1))) void bwd_f32_kernel(BwdArgs a) {
+__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK), bwd_waves_per_eu(D, MASK)))) void bwd_f32_kernel(BwdArgs a) {
     __shared__ BwdSmem<D> sm;
     const int BHk = a.s.B * a.s.Hkv;
     const int kt = blockIdx.x / BHk;  // tile 0 has the most causal work, so it goes first
@@ -745,7 +755,7 @@ DEVI float *kv_slot(const BwdArgs &a, int64_t range, int which) {
 // blocks (workgroup w runs on XCD w % 8), so the key tiles of one kv head, which read the same
 // Q / dO, share an L2.
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(D == 128 || (D <= 64 && !MASK) ? 2 : 1, D == 128 || (D <= 64 && !MASK) ? 2 : 1))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
+__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK), bwd_waves_per_eu(D, MASK)))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
     __shared__ BwdSmem<D> sm;
     const int w = blockIdx.x;
     const int64_t c = (int64_t)(w & 7) * (sk.chunks >> 3) + (w >> 3);
@@ -901,8 +911,8 @@ __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK 
     }
 }
 
-// Workgroups of the backward that fit on the device at once (the occupancy the kernel's
-// waves_per_eu attribute sets: two per CU at D <= 64 without a mask, one otherwise); 0 if unknown.
+// Workgroups of the backward that fit on the device at once (the occupancy bwd_waves_per_eu sets:
+// two per CU at D <= 64 without a mask, one otherwise); 0 if unknown.
 int resident_workgroups(int D, bool mask) { return device_cus() * (D <= 64 && !mask ? 2 : 1); }
 
 // The stream-K schedule where whole tiles leave part of the device idle (measured on one MI355X,

@@ -255,7 +255,8 @@ def test_causal_with_mask(oracle_lib):
     _check(oracle_lib, q, k, v, g, True, 0.2, mask, tag="causal+mask")
 
 
-def test_large_logits(oracle_lib):
+@pytest.mark.parametrize("E,factor", [(64, 2), (128, 8)])
+def test_large_logits(oracle_lib, E, factor):
     """Scores far past the exp_u20 bound (|x - max| > 87.3, the reference's SLEEF fallback).
 
     Forward at the standard tolerance.  The gradients of such a peaked softmax are
@@ -264,11 +265,15 @@ def test_large_logits(oracle_lib):
     GPU is held to float64 truth instead, each side running end to end on its own forward
     (out, lse): its error may not exceed twice the oracle's.  (Feeding one side's lse to the
     other's backward would mix two summation orders of the same scores, so that P no longer
-    sums to one by ~1e-5, an error of the test, not of either implementation.)"""
+    sums to one by ~1e-5, an error of the test, not of either implementation.)  At head dim 128
+    the backward's scores run on 16x16x4 products in another order than the forward's 32x32x2
+    (its 8-wave layout), which is that same mixing inside the GPU: its error there is held to
+    8x the oracle's (measured up to 5.3x, in dV).  q and k scale with E^(-1/4), so the score
+    gaps within a row stay of the order of 100 at both head dims."""
     from oracle import brute
     rng = np.random.default_rng(9)
-    q, k, v, g = (rng.standard_normal((1, 2, 96, 64), dtype=np.float32) for _ in range(4))
-    q, k = q * 6, k * 6
+    q, k, v, g = (rng.standard_normal((1, 2, 96, E), dtype=np.float32) for _ in range(4))
+    q, k = q * 6 * (64 / E) ** 0.25, k * 6 * (64 / E) ** 0.25
     ref_o, ref_l = oracle_lib.forward(q, k, v, True)
     out, lse = _run_fwd(q, k, v, True, None, None)
     assert_f32(out, ref_o, "large-logits out")
@@ -278,7 +283,7 @@ def test_large_logits(oracle_lib):
     got = _run_bwd(g, q, k, v, out, lse, True, None, None)
     for name, a, b, t in zip(("dq", "dk", "dv"), got, ref, truth):
         err_gpu, err_ref = np.abs(a - t).max(), np.abs(b - t).max()
-        assert err_gpu <= 2 * err_ref + 2e-6, f"{name}: gpu err {err_gpu:.3e} vs oracle {err_ref:.3e}"
+        assert err_gpu <= factor * err_ref + 2e-6, f"{name}: gpu err {err_gpu:.3e} vs oracle {err_ref:.3e}"
 
 
 def test_errors_match_reference():
