@@ -111,6 +111,22 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
     constexpr int RPL = 64 / C;          // rows per wave-wide load
     constexpr int ROWS = BN / W;         // rows per wave
     static_assert(ROWS % RPL == 0, "a wave loads whole rows");
+    if (n0 + BN <= S) {
+        // No row to clamp: the tile's base in SGPRs and a lane offset that is the same for
+        // every tile (hoisted out of the tile loop), so the transfers cost no VALU instructions
+        // (float32 MFMAs and VALU instructions do not overlap; the clamped addresses took ~6
+        // per transfer).
+        const float *kt = kb + (int64_t)n0 * D, *vt = vb + (int64_t)n0 * D;
+#pragma unroll
+        for (int j = 0; j < ROWS / RPL; ++j) {
+            const int r0 = wave * ROWS + j * RPL;
+            const int row = r0 + lane / C;
+            const uint32_t off = (uint32_t)(row * D + (((lane % C) ^ swz<D>(row)) << 2)) * 4u;
+            if constexpr (DO_K) lds_dma16_off(kt, off, &sm.k[r0][0]);
+            if constexpr (DO_V) lds_dma16_off(vt, off, &sm.v[r0][0]);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < ROWS / RPL; ++j) {
         const int r0 = wave * ROWS + j * RPL;
