@@ -472,10 +472,10 @@ __global__ __launch_bounds__(256) void dropout_apply4_kernel(const uint32_t *bit
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= n4) return;
     const uint32_t b = bits[t >> 3] >> (4 * (t & 7));
-    f32x4 v = x[t];
+    f32x4 v = load_nt(x + t);  // x and y stream through once
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = v[c] * ((b >> c & 1u) ? scale : 0.0f);
-    y[t] = v;
+    __builtin_nontemporal_store(v, y + t);
 }
 
 }  // namespace

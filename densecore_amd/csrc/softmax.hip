@@ -54,8 +54,8 @@ DEVI void load_row(const float *src, const float *msk, int W, int lane, float (&
             const int j = 4 * lane + 256 * i;
             f32x4 t = {pad, pad, pad, pad};
             if (j < W) {
-                t = *reinterpret_cast<const f32x4 *>(src + j);
-                if (MASK) t += *reinterpret_cast<const f32x4 *>(msk + j);
+                t = load_nt(reinterpret_cast<const f32x4 *>(src + j));  // read once
+                if (MASK) t += *reinterpret_cast<const f32x4 *>(msk + j);  // shared by rows
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[4 * i + c] = t[c];
@@ -76,7 +76,9 @@ DEVI void store_row(float *dst, int W, int lane, const float (&v)[NV * 4]) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int j = 4 * lane + 256 * i;
-            if (j < W) *reinterpret_cast<f32x4 *>(dst + j) = {v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+            if (j < W)
+                __builtin_nontemporal_store(f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]},
+                                            reinterpret_cast<f32x4 *>(dst + j));
         }
     } else {
 #pragma unroll
