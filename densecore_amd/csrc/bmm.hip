@@ -7,16 +7,21 @@
 // math attention path's two products (q k^T, a transposed view of k, and weights v) and MHA's.
 //
 // Blocking (this kernel's own): a workgroup of 4 waves computes a BM x BN tile of one batch item
-// (waves 2 x 2, each (BM/2) x (BN/2) as 32 x 32 MFMA tiles), over k in steps of BK = 32.  A and B
+// (waves 2 x 2, each (BM/2) x (BN/2) as 32 x 32 MFMA tiles), over k in steps of BK.  A and B
 // tiles are staged in LDS k-major ([k][m], [k][n]), so an MFMA operand is 32 consecutive floats
 // per half-wave (lane l takes A[m = l % 32][k = l / 32] and B[k = l / 32][n = l % 32]).  Global
 // loads follow the operand's contiguous dimension: 16-byte loads along m or n are stored as they
 // are; 16-byte loads along k are stored transposed (lanes along m or n, conflict-free); other
 // layouts load one element per lane.  The next k tile is loaded into registers while the current
-// one is multiplied (one barrier per k tile).  Accumulation is float32 (the reference sums the
-// products in k order; here the MFMA's order, within the float32 tolerance).  The launcher also
-// serves the attention path of head dims above 128 (wide.hip), which writes C through strides
-// and can add A B into C.
+// one is multiplied (one barrier per k tile).  Where every tile has the same k extent (no causal
+// trimming of k) BK = 16: half the LDS of BK = 32, so four workgroups run per CU and four waves per
+// SIMD hide the loads' latency (on one MI355X, 32 items of 2048 x 256 x 2048: 705 -> 598 us; 256
+// items of 512 x 64 x 512: 148 -> 134 us).  Products whose tiles stop k at the diagonal (causal
+// modes 2 and 3) keep BK = 32 and two workgroups per CU: their longest tiles set the time, and
+// sharing a SIMD four ways slowed them (D = 256 causal P V 529 -> 610 us).  Accumulation is
+// float32 (the reference sums the products in k order; here the MFMA's order, within the float32
+// tolerance).  The launcher also serves the attention path of head dims above 128 (wide.hip),
+// which writes C through strides and can add A B into C.
 #include "common.hpp"
 #include "params.hpp"
 
@@ -24,10 +29,9 @@ namespace dc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int BK = 32;
 constexpr int kPad = 4;  // LDS row padding (floats): keeps 16-byte stores aligned
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 struct alignas(16) BmmSmem {
     float a[2][BK][BM + kPad];
     float b[2][BK][BN + kPad];
@@ -39,7 +43,7 @@ enum Layout { CONTIG_K = 0, CONTIG_MN = 1, SCALAR = 2 };
 
 // The register stage of one operand tile: R rows (m or n) by BK, from `p` (the batch item's base)
 // with strides (s_r along the rows, s_k along k); rows past `rows` and k past `kk` read zero.
-template <int R, int L>
+template <int R, int L, int BK>
 struct Stage {
     static constexpr int N = R * BK / (L == SCALAR ? 1 : 4) / kThreads;
     static_assert(N >= 1, "tile too small for the workgroup");
@@ -96,11 +100,11 @@ struct Stage {
     }
 };
 
-template <int BM, int BN, int LA, int LB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bmm_f32_kernel(BmmArgs g) {
+template <int BM, int BN, int LA, int LB, int BK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BK == 16 ? 4 : 2, BK == 16 ? 4 : 2))) void bmm_f32_kernel(BmmArgs g) {
     constexpr int TM = BM / 64, TN = BN / 64;  // 32 x 32 MFMA tiles per wave along m, n
     static_assert(TM >= 1 && TN >= 1, "a wave covers at least 32 x 32");
-    __shared__ BmmSmem<BM, BN> sm;
+    __shared__ BmmSmem<BM, BN, BK> sm;
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, gh = lane >> 5;
     const int wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int mt = (g.m + BM - 1) / BM, nt = (g.n + BN - 1) / BN, per = mt * nt;
@@ -128,8 +132,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         return kt;
     };
 
-    Stage<BM, LA> sa;
-    Stage<BN, LB> sb;
+    Stage<BM, LA, BK> sa;
+    Stage<BN, LB, BK> sb;
     int kt = next_live(0);
     // B's "rows" are its n columns: its row stride is the n stride, its k stride the k stride.
     sa.load(ap, g.sam, g.sak, m0, g.m, kt * BK, kk, tid);
@@ -208,21 +212,27 @@ int layout_b(const BmmArgs &g) {
     return SCALAR;
 }
 
-template <int BM, int BN, int LA>
+template <int BM, int BN, int LA, int BK>
 hipError_t launch_b(const BmmArgs &g, int lb, dim3 grid, hipStream_t st) {
-    if (lb == CONTIG_K) return launch(bmm_f32_kernel<BM, BN, LA, CONTIG_K>, grid, dim3(kThreads), st, g);
-    if (lb == CONTIG_MN) return launch(bmm_f32_kernel<BM, BN, LA, CONTIG_MN>, grid, dim3(kThreads), st, g);
-    return launch(bmm_f32_kernel<BM, BN, LA, SCALAR>, grid, dim3(kThreads), st, g);
+    if (lb == CONTIG_K) return launch(bmm_f32_kernel<BM, BN, LA, CONTIG_K, BK>, grid, dim3(kThreads), st, g);
+    if (lb == CONTIG_MN) return launch(bmm_f32_kernel<BM, BN, LA, CONTIG_MN, BK>, grid, dim3(kThreads), st, g);
+    return launch(bmm_f32_kernel<BM, BN, LA, SCALAR, BK>, grid, dim3(kThreads), st, g);
 }
 
-template <int BM, int BN>
-hipError_t launch_t(const BmmArgs &g, hipStream_t st) {
+template <int BM, int BN, int BK>
+hipError_t launch_k(const BmmArgs &g, hipStream_t st) {
     const int64_t tiles = (int64_t)((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN) * g.batch;
     const dim3 grid((unsigned)tiles);
     const int la = layout_a(g), lb = layout_b(g);
-    if (la == CONTIG_K) return launch_b<BM, BN, CONTIG_K>(g, lb, grid, st);
-    if (la == CONTIG_MN) return launch_b<BM, BN, CONTIG_MN>(g, lb, grid, st);
-    return launch_b<BM, BN, SCALAR>(g, lb, grid, st);
+    if (la == CONTIG_K) return launch_b<BM, BN, CONTIG_K, BK>(g, lb, grid, st);
+    if (la == CONTIG_MN) return launch_b<BM, BN, CONTIG_MN, BK>(g, lb, grid, st);
+    return launch_b<BM, BN, SCALAR, BK>(g, lb, grid, st);
+}
+
+// BK = 16 (four workgroups per CU) unless the causal mode trims k per tile.
+template <int BM, int BN>
+hipError_t launch_t(const BmmArgs &g, hipStream_t st) {
+    return g.causal_mode >= 2 ? launch_k<BM, BN, 32>(g, st) : launch_k<BM, BN, 16>(g, st);
 }
 
 // Zeroes C when k == 0 (the reference returns zeros); C is (batch, m, n) through its strides.
