@@ -286,6 +286,27 @@ def test_large_logits(oracle_lib, E, factor):
         assert err_gpu <= factor * err_ref + 2e-6, f"{name}: gpu err {err_gpu:.3e} vs oracle {err_ref:.3e}"
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_nan_scores_propagate(oracle_lib, causal):
+    """A NaN in q or k makes every row that sees it NaN, out and lse, as the reference's
+    NaN-propagating row max does (src/torch_attention.rs:42-87, src/torch_softmax.rs:43-54); a
+    causally hidden NaN key leaves the rows before it untouched (its score is -inf either way).
+    (NaN in v, or the backward, also reach rows through 0 * NaN inside a tile whose keys a row does
+    not see; which rows depends on each implementation's tiling, so those are not compared.)"""
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((1, 2, 70, 16), dtype=np.float32) for _ in range(3))
+    k[0, 1, 5, 3] = np.nan
+    k[0, 0, 60, 2] = np.nan
+    q[0, 1, 33, 0] = np.nan
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    out, lse = _run_fwd(q, k, v, causal, None, None)
+    assert (np.isnan(out) == np.isnan(ref_o)).all() and (np.isnan(lse) == np.isnan(ref_l)).all()
+    assert np.isnan(ref_l).sum() == (70 + 70 if not causal else 10 + 65)
+    fin = ~np.isnan(ref_o)
+    assert_f32(out[fin], ref_o[fin], "finite out")
+    assert_f32(lse[~np.isnan(ref_l)], ref_l[~np.isnan(ref_l)], "finite lse")
+
+
 def test_errors_match_reference():
     """src/lib.rs:561-571, 599-606, 658-663: ValueError with the reference's messages."""
     from densecore_amd import _native
