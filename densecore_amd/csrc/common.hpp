@@ -200,6 +200,36 @@ DEVI void lds_dma16_off(const void *base, uint32_t off, void *dst) {
                  : "memory");
 }
 
+// A wave-uniform global address as an SGPR pair (each half read from the first lane).
+DEVI uint64_t sgpr_addr(const void *p) {
+    const uint64_t x = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// The LDS byte address of a pointer into LDS: cast once and reused, it spares each transfer the
+// null test of a generic-to-LDS conversion.
+DEVI uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
+}
+
+// Two saddr-form transfers (global base g + lane offset off, into LDS address l) in one statement,
+// m0 saved before the first and restored after the second: three SALU instructions per transfer
+// instead of lds_dma16_off's seven.
+DEVI void lds_dma16_pair(uint64_t g0, uint32_t off0, uint32_t l0, uint64_t g1, uint32_t off1, uint32_t l1) {
+    l0 = __builtin_amdgcn_readfirstlane(l0), l1 = __builtin_amdgcn_readfirstlane(l1);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
+                 "s_mov_b32 m0, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %5, %6\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(l0), "v"(off0), "s"(g0), "s"(l1), "v"(off1), "s"(g1)
+                 : "memory");
+}
+
 // A global load marked nontemporal (global_load ... nt): for data a kernel streams once.  On one
 // MI355X a read of 4 GiB in 16-byte loads ran at 7.1 TB/s this way against 6.3 TB/s without.
 template <typename V>

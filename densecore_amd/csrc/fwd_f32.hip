@@ -117,11 +117,30 @@ DEVI void issue_tile(FwdSmemAsync<D, BN> &sm, const float *kb, const float *vb, 
         // (float32 MFMAs and VALU instructions do not overlap; the clamped addresses took ~6
         // per transfer).
         const float *kt = kb + (int64_t)n0 * D, *vt = vb + (int64_t)n0 * D;
+        constexpr int NJ = ROWS / RPL;
+        auto lane_off = [&](int j) {
+            const int row = wave * ROWS + j * RPL + lane / C;
+            return (uint32_t)(row * D + (((lane % C) ^ swz<D>(row)) << 2)) * 4u;
+        };
+        if constexpr (W == 1 && (DO_K != DO_V)) {
+            // One-wave workgroups (K or V alone): transfers in pairs, one m0 save per pair and the
+            // LDS address cast once (B64 H6 L256 causal 41.4 -> 40.5 us; the 4-wave kernels, whose
+            // wave index the LDS addresses carry, measured ~1% slower this way).
+            const uint64_t gb = sgpr_addr(DO_K ? kt : vt);
+            const uint32_t lb = lds_addr(DO_K ? &sm.k[0][0] : &sm.v[0][0]);
 #pragma unroll
-        for (int j = 0; j < ROWS / RPL; ++j) {
+            for (int j = 0; j + 1 < NJ; j += 2)
+                lds_dma16_pair(gb, lane_off(j), lb + (uint32_t)(j * RPL * D * 4), gb, lane_off(j + 1),
+                               lb + (uint32_t)((j + 1) * RPL * D * 4));
+            if constexpr (NJ % 2 == 1)
+                lds_dma16_off(DO_K ? kt : vt, lane_off(NJ - 1),
+                              DO_K ? &sm.k[(NJ - 1) * RPL][0] : &sm.v[(NJ - 1) * RPL][0]);
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
             const int r0 = wave * ROWS + j * RPL;
-            const int row = r0 + lane / C;
-            const uint32_t off = (uint32_t)(row * D + (((lane % C) ^ swz<D>(row)) << 2)) * 4u;
+            const uint32_t off = lane_off(j);
             if constexpr (DO_K) lds_dma16_off(kt, off, &sm.k[r0][0]);
             if constexpr (DO_V) lds_dma16_off(vt, off, &sm.v[r0][0]);
         }
