@@ -53,7 +53,7 @@ struct alignas(16) BwdSmem {
     float q[kBM][D + 4];         // read along d with ds_read_b128 per lane: padded rows
     float dout[kBM][D + 4];
     float ds[kBM][kBN + 4];      // dS of the step, all four waves' keys
-    float lse[kBM];              // times log2 e
+    float lse[kBM];
     float dsum[kBM];
 };
 
@@ -87,7 +87,7 @@ struct QStage {
         }
         if (tid < kBM) {
             const int qq = m0 + tid;
-            lse = qq < L ? lseb[qq] * kLog2e : INFINITY;
+            lse = qq < L ? lseb[qq] : INFINITY;
             dsum = qq < L ? dsumb[qq] : 0.f;
         }
     }
@@ -114,7 +114,7 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
     }
     if (tid < kBM) {
         const int qq = m0 + tid;
-        sm.lse[tid] = qq < L ? lseb[qq] * kLog2e : INFINITY;
+        sm.lse[tid] = qq < L ? lseb[qq] : INFINITY;
         sm.dsum[tid] = qq < L ? dsumb[qq] : 0.f;
     }
 }
@@ -351,7 +351,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         // S = Q K^T and dP = dO V^T: rows are queries, columns are this wave's keys.
         f32x16 sacc, pacc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = -sm.dsum[acc_row(r, g)];
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f, pacc[r] = 0.f;
 #pragma unroll
         for (int t4 = 0; t4 < DH; t4 += 4) {
             const f32x4 qq = *reinterpret_cast<const f32x4 *>(&sm.q[lr][g * DH + t4]);
@@ -369,14 +369,11 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int qrow = acc_row(r, g), qq = m0 + qrow;
-            // Base-2 exponent: q.k times scale log2 e minus lse log2 e (staged so) in one FMA,
-            // the forward's form (with a mask, scale * q.k + mask, then the FMA with log2 e).
-            if (MASK) {
-                const float x = sacc[r] * s.scale + ((qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f);
-                sacc[r] = exp2_fast(fmaf(x, kLog2e, -sm.lse[qrow]));
-            } else {
-                sacc[r] = exp2_fast(fmaf(sacc[r], s.scale_log2, -sm.lse[qrow]));
-            }
+            // scale * q.k (+ mask) - lse in natural-log units, as the reference forms it,
+            // then one conversion to base 2 for v_exp_f32.
+            float x = sacc[r] * s.scale;
+            if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+            sacc[r] = exp2_fast((x - sm.lse[qrow]) * kLog2e);
         }
         // Keys past the end or (causal) past a query only occur when the wave's keys reach the
         // end of the sequence or cross the diagonal of this query tile: a wave-uniform branch,
@@ -391,7 +388,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int qrow = acc_row(r, g);
-            pacc[r] = sacc[r] * pacc[r];  // dP accumulated onto -dsum
+            pacc[r] = sacc[r] * (pacc[r] - sm.dsum[qrow]);
             sm.ds[qrow][wave * 32 + lr] = pacc[r];
         }
 
@@ -588,10 +585,7 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         // compiler reads all of them up front and runs out of registers).
         f32x4 sacc[2], pacc[2];
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {  // dP accumulates onto -dsum
-            sacc[qh] = f32x4{0.f, 0.f, 0.f, 0.f};
-            pacc[qh] = -*reinterpret_cast<const f32x4 *>(&sm.dsum[16 * qh + 4 * c4]);
-        }
+        for (int qh = 0; qh < 2; ++qh) sacc[qh] = f32x4{0.f, 0.f, 0.f, 0.f}, pacc[qh] = f32x4{0.f, 0.f, 0.f, 0.f};
         f32x4 qop[2][2], oop[2][2], kop[2];  // [buffer][query half]; K: [buffer]
         auto read_qo = [&](int j, int buf) {
 #pragma unroll
@@ -617,19 +611,19 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         }
 
         // P and dS, elementwise in the accumulator layout (rows 16 qh + 4 c4 + v); dS goes to the
-        // shared tile.  The exponent as in key_tile.
+        // shared tile.  scale * q.k (+ mask) - lse in natural-log units, then one conversion to
+        // base 2, as in key_tile.
+        f32x4 dsum4[2];
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
             const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&sm.lse[16 * qh + 4 * c4]);
+            dsum4[qh] = *reinterpret_cast<const f32x4 *>(&sm.dsum[16 * qh + 4 * c4]);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int qq = m0 + 16 * qh + 4 * c4 + v;
-                if (MASK) {
-                    const float x = sacc[qh][v] * s.scale + ((qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f);
-                    sacc[qh][v] = exp2_fast(fmaf(x, kLog2e, -l4[v]));
-                } else {
-                    sacc[qh][v] = exp2_fast(fmaf(sacc[qh][v], s.scale_log2, -l4[v]));
-                }
+                float x = sacc[qh][v] * s.scale;
+                if (MASK) x += (qq < s.L && key < s.S) ? mbase[(int64_t)qq * s.msl + key] : 0.f;
+                sacc[qh][v] = exp2_fast((x - l4[v]) * kLog2e);
             }
         }
         // Keys past the end or (causal) past a query only occur on the edge steps: a
@@ -646,7 +640,7 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                pacc[qh][v] = sacc[qh][v] * pacc[qh][v];
+                pacc[qh][v] = sacc[qh][v] * (pacc[qh][v] - dsum4[qh][v]);
                 sm.ds[16 * qh + 4 * c4 + v][wave * 16 + r16] = pacc[qh][v];
             }
 
