@@ -335,7 +335,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
             // LDS slot.
             const uint64_t open = __ballot(mcur != -INFINITY);
             float *slot = mslot[wave];
-            slot[lane] = mcur;
+            slot[lane] = mcur * kLog2e;  // in log2 units: one multiply per key, not per score
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt) {
                 live[kt] = live[kt] && ((open >> (32 * kt)) & 0xffffffffull) != 0;
@@ -410,7 +410,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(D <= 64 
         }
         // Scores in log2 units (with a mask; without one the raw products, see csc), masked on
         // edge tiles; tile max per query.
-        if constexpr (MASK) {
+        // A row mask arrives times log2 e, so its score is one FMA with scale log2 e (bit-identical
+        // to the two-step form when the scale is a power of two, as at head dims 16, 64 and 256;
+        // B16 H16 L512 key padding 101.7 -> 99.9 us).
+        if constexpr (ROWMASK) {
+#pragma unroll
+            for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kt][r] = fmaf(sacc[kt][r], s.scale_log2, mv[kt][r]);
+        } else if constexpr (MASK) {
 #pragma unroll
             for (int kt = 0; kt < NT; ++kt)
 #pragma unroll
