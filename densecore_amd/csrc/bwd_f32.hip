@@ -875,19 +875,32 @@ __global__ __launch_bounds__(256) void bwd_reduce_f32_kernel(BwdArgs a, StreamK 
         const int bh = (int)(row / s.L), r = (int)(row % s.L);
         const int last = s.causal ? min(nkt - 1, r / kBN) : nkt - 1;  // tiles whose steps cover r
         const bool vec = vec4;
+        // The slots are loaded in groups of kGroup before they are added, in tile order (the sum
+        // does not depend on the grouping).  Against one load and add per iteration the pass
+        // measured the same time in a same-box comparison: the resident waves already keep
+        // enough loads in flight.
+        constexpr int kGroup = 8;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        int64_t before = 0;  // slot_before(kt), accumulated
-        for (int kt = 0; kt <= last; ++kt) {
-            const int rf = slot_from(s, kt);
-            const float *src = a.dq_part + ((before * BH) + (int64_t)bh * (s.L - rf) + (r - rf)) * s.E + d0;
-            if (vec) {
-                acc += load_nt(reinterpret_cast<const f32x4 *>(src));  // each slot is read once
-            } else {
+        for (int k0 = 0; k0 <= last; k0 += kGroup) {
+            f32x4 part[kGroup];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (d0 + e < s.E) acc[e] += src[e];
+            for (int u = 0; u < kGroup; ++u) {
+                const int kt = k0 + u;
+                if (kt > last) break;
+                const int rf = slot_from(s, kt);
+                const float *src = a.dq_part + (slot_before(s, kt) * BH + (int64_t)bh * (s.L - rf) + (r - rf)) * s.E + d0;
+                if (vec) {
+                    part[u] = load_nt(reinterpret_cast<const f32x4 *>(src));  // each slot is read once
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) part[u][e] = d0 + e < s.E ? src[e] : 0.f;
+                }
             }
-            before += s.L - rf;
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                if (k0 + u > last) break;
+                acc += part[u];
+            }
         }
         float *dst = static_cast<float *>(a.dq) + row * s.E + d0;
         if (vec) {
