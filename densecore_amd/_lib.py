@@ -40,7 +40,7 @@ class Schedule(ctypes.Structure):
                 ("streamk_ranges", ctypes.c_int32), ("split_chunk_k", ctypes.c_int32),
                 ("split_chunk_q", ctypes.c_int32), ("f16_products", ctypes.c_int32),
                 ("deterministic", ctypes.c_int32), ("materialized_rows", ctypes.c_int32),
-                ("workgroups", ctypes.c_int64)]
+                ("workgroups", ctypes.c_int64), ("chunks", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

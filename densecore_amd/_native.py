@@ -11,6 +11,7 @@ ordered on torch's current stream of the tensors' device.
 ``_flash_decode`` is the new single-query entry point (split-KV), equivalent to
 ``_flash_attention`` at L = 1 without causal masking.
 """
+import collections
 import math
 
 import torch
@@ -79,18 +80,49 @@ def _stream(dev):
 
 
 # One workspace per (device, stream), grown on demand and reused: calls on one stream run in
-# order, so a call never overlaps the previous user of its stream's workspace.
-_WORKSPACES = {}
+# order, so a call never overlaps the previous user of its stream's workspace.  At most
+# _MAX_WORKSPACES streams keep one (the least recently used is dropped; torch's caching allocator
+# frees its memory once the last call using it has run), and release_workspaces() drops them all.
+# Under stream capture (a CUDA graph) every call gets a workspace of its own instead: a captured
+# graph keeps its addresses, and two graphs replayed on different streams must not share one.
+_WORKSPACES = collections.OrderedDict()
+_MAX_WORKSPACES = 4
+
+
+def release_workspaces():
+    """Drop every cached workspace (their memory returns to torch's caching allocator)."""
+    _WORKSPACES.clear()
 
 
 def _workspace(nbytes, dev):
     nbytes = max(int(nbytes), 1)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=dev)
     key = (dev.index, _stream(dev))
-    ws = _WORKSPACES.get(key)
+    ws = _WORKSPACES.pop(key, None)
     if ws is None or ws.numel() < nbytes:
+        ws = None  # release the smaller buffer before allocating its replacement
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
+    _WORKSPACES[key] = ws
+    while len(_WORKSPACES) > _MAX_WORKSPACES:
+        _WORKSPACES.popitem(last=False)
     return ws
+
+
+# The float32 backward's full workspace holds one dQ-sized slot per 128-key tile (for sums in a
+# fixed order), which grows as S / 128 * |dq|: about 4 GiB at B1 H32 L=S=8192 E128 causal.  Above
+# max(this many bytes, 8 |dq|) a call passes that bound instead; the library then runs the problem
+# in pieces (whole batches, or kv heads of one batch) whose slots fit, with the same fixed-order
+# sums, and only when not even one kv head's slots fit, with float atomics.
+DETERMINISTIC_WORKSPACE_BYTES = 1 << 30
+
+
+def _bwd_workspace_bytes(L_, d, dims, dtype):
+    full = int(L_.dc_sdpa_bwd_workspace_size(d))
+    B, H, _, L, _, E = dims
+    if dtype != torch.float32 or E > 128:
+        return full
+    return min(full, max(DETERMINISTIC_WORKSPACE_BYTES, 8 * B * H * L * E * 4))
 
 
 def _schedule(backward, q, k, v, causal, scale=None, mask=None, workspace_bytes=None):
@@ -102,8 +134,9 @@ def _schedule(backward, q, k, v, causal, scale=None, mask=None, workspace_bytes=
     d = _desc(dims, causal, scale, dtype, ms)
     L_ = _lib.lib()
     if workspace_bytes is None:
-        size = L_.dc_sdpa_bwd_workspace_size if backward else L_.dc_sdpa_fwd_workspace_size
-        workspace_bytes = max(int(size(d)), 1)
+        size = (_bwd_workspace_bytes(L_, d, dims, dtype) if backward
+                else int(L_.dc_sdpa_fwd_workspace_size(d)))
+        workspace_bytes = max(size, 1)
     out = _lib.Schedule()
     query = L_.dc_sdpa_bwd_schedule if backward else L_.dc_sdpa_fwd_schedule
     _lib.check(query(d, int(mask is not None), int(workspace_bytes), out))
@@ -144,7 +177,7 @@ def _flash_attention_backward(grad_out, q, k, v, out, lse, causal, scale=None, m
     dv = torch.empty((B, Hkv, S, E), dtype=dtype, device=dev)
     d = _desc(dims, causal, scale, dtype, ms)
     L_ = _lib.lib()
-    ws = _workspace(L_.dc_sdpa_bwd_workspace_size(d), dev)
+    ws = _workspace(_bwd_workspace_bytes(L_, d, dims, dtype), dev)
     _lib.check(L_.dc_sdpa_bwd(d, _ptr(grad_out), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
                               _ptr(mask), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(),
                               _stream(dev)))

@@ -194,6 +194,75 @@ size_t bwd_ws(const dc::AttnShape &s, bool bf16) { return bwd_layout(s, bf16).to
 // copies are used only when they fit.
 size_t bwd_ws_min(const dc::AttnShape &s) { return bwd_layout(s, false).part; }
 
+// The float32 backward over a piece of the problem: nb whole batches from b0, or (nb == 0) nh kv
+// heads of batch b0 from kv head hk0.  Each is contiguous in every tensor, so the piece is the
+// same backward over offset pointers; dsum and lse keep the whole problem's layout.
+dc::BwdArgs bwd_piece(const dc::BwdArgs &a, int b0, int nb, int hk0, int nh) {
+    const dc::AttnShape &s = a.s;
+    dc::BwdArgs c = a;
+    const int h0 = hk0 * s.repeat;
+    if (nb > 0) {
+        c.s.B = nb;
+    } else {
+        c.s.B = 1, c.s.Hkv = nh, c.s.H = nh * s.repeat;
+    }
+    const int64_t qrow = (int64_t)b0 * s.H + h0, krow = (int64_t)b0 * s.Hkv + hk0;
+    const int64_t qoff = qrow * s.L * s.E, koff = krow * s.S * s.E;
+    auto off = [](const void *p, int64_t n) -> const void * {
+        return p ? static_cast<const float *>(p) + n : nullptr;
+    };
+    auto offw = [](void *p, int64_t n) -> void * { return p ? static_cast<float *>(p) + n : nullptr; };
+    c.dout = off(a.dout, qoff), c.q = off(a.q, qoff), c.out = off(a.out, qoff);
+    c.k = off(a.k, koff), c.v = off(a.v, koff);
+    c.dq = offw(a.dq, qoff), c.dk = offw(a.dk, koff), c.dv = offw(a.dv, koff);
+    c.dq_acc = static_cast<float *>(c.dq);
+    c.lse = a.lse + qrow * s.L;
+    c.dsum = a.dsum + qrow * s.L;
+    if (s.mask) c.s.mask = s.mask + (int64_t)b0 * s.msb + (int64_t)h0 * s.msh;
+    c.s.vec = s.vec && aligned16(c.dout) && aligned16(c.q) && aligned16(c.out) && aligned16(c.k) &&
+              aligned16(c.v) && aligned16(c.dq) && aligned16(c.dk) && aligned16(c.dv);
+    return c;
+}
+
+// The float32 backward when `avail` bytes of partials (after dsum) are less than the whole
+// problem needs for a result identical from run to run: pieces of whole batches, or of one
+// batch's kv heads, each small enough for its partials to fit, run one after another on the
+// same stream (each piece is a full backward, so the sums keep their fixed order); if not even
+// one kv head fits, the whole problem runs once with float atomics.
+dc_status bwd_f32_chunked(const dc::BwdArgs &a, size_t avail, hipStream_t st) {
+    const dc::AttnShape &s = a.s;
+    auto fits = [&](int nb, int nh) { return dc::bwd_f32_part_bytes(bwd_piece(a, 0, nb, 0, nh).s) <= avail; };
+    // The largest piece that fits, stepping down from an estimate (the dQ slots grow linearly with
+    // the piece; the stream-K slots of small grids add a bounded amount).
+    auto largest = [&](int n, auto fit) {
+        int k = n - 1;
+        while (k >= 1 && !fit(k)) k -= std::max(1, k / 16);
+        return k;
+    };
+    const int nb = avail > 0 && s.B > 1 ? largest(s.B, [&](int k) { return fits(k, 0); }) : 0;
+    const int nh = avail == 0 || nb >= 1 ? 0 : largest(s.Hkv, [&](int k) { return fits(0, k); });
+    dc::BwdArgs whole = a;
+    if (nb < 1 && nh < 1) {  // float atomics over the whole problem
+        whole.dq_part = nullptr, whole.part_bytes = 0;
+        return launched(dc::launch_bwd_f32(whole, st));
+    }
+    int pieces = 0;
+    if (nb >= 1) {
+        for (int b0 = 0; b0 < s.B; b0 += nb, ++pieces) {
+            dc_status r = launched(dc::launch_bwd_f32(bwd_piece(a, b0, std::min(nb, s.B - b0), 0, 0), st));
+            if (r != DC_OK) return r;
+        }
+    } else {
+        for (int b0 = 0; b0 < s.B; ++b0)
+            for (int hk0 = 0; hk0 < s.Hkv; hk0 += nh, ++pieces) {
+                dc_status r = launched(dc::launch_bwd_f32(bwd_piece(a, b0, 0, hk0, std::min(nh, s.Hkv - hk0)), st));
+                if (r != DC_OK) return r;
+            }
+    }
+    record_schedule(chunks, pieces);
+    return ok();
+}
+
 size_t decode_ws(const dc::AttnShape &s, bool bf16) {
     if (s.E > dc::kDecodeMaxHeadDim) return dc::wide_ws_bytes(s, bf16, false);
     int split_len = 0;
@@ -232,6 +301,14 @@ dc_status check_softmax(const dc_softmax_desc *d, const float *mask, dc::Softmax
         a->msl = d->mask_stride_l;
     }
     return ok();
+}
+
+// A decode launch, then the rows a NaN scale fixes (the decode path is non-causal).
+dc_status decode_then_ref_rows(const dc::DecodeArgs &a, bool bf16, hipStream_t st) {
+    dc_status r = launched(dc::launch_decode(a, bf16, st));
+    if (r != DC_OK) return r;
+    const dc::FwdArgs f{a.s, a.q, a.k, a.v, a.out, a.lse, nullptr, nullptr, nullptr, nullptr, nullptr};
+    return launched(dc::launch_fwd_ref_rows(f, bf16, st));
 }
 
 bool softmax_vec(const dc::SoftmaxArgs &a, const void *p0, const void *p1, const void *p2) {
@@ -296,7 +373,10 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
             return fail(DC_INVALID_ARGUMENT,
                         "flash attention forward with head_dim above 128 needs a workspace of "
                         "dc_sdpa_fwd_workspace_size bytes (at least one row of scores per kv head)");
-        return launched(dc::launch_wide_fwd(a, bf16, workspace, workspace_bytes, static_cast<hipStream_t>(stream)));
+        hipStream_t strm = static_cast<hipStream_t>(stream);
+        dc_status st2 = launched(dc::launch_wide_fwd(a, bf16, workspace, workspace_bytes, strm));
+        if (st2 != DC_OK) return st2;
+        return launched(dc::launch_fwd_ref_rows(a, bf16, strm));
     }
     // A workspace too small (or none) only gives up the longest-first order of key-padding masks,
     // the split key ranges of small grids, and for bf16 the fp16 P V product (the bf16 hi + lo
@@ -322,8 +402,9 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         }
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
-    if (d->dtype == DC_F32) return launched(dc::launch_fwd_f32(a, strm));
-    return launched(dc::launch_fwd_bf16(a, strm));
+    st = launched(d->dtype == DC_F32 ? dc::launch_fwd_f32(a, strm) : dc::launch_fwd_bf16(a, strm));
+    if (st != DC_OK) return st;
+    return launched(dc::launch_fwd_ref_rows(a, d->dtype == DC_BF16, strm));
 }
 
 size_t dc_sdpa_bwd_workspace_size(const dc_attn_desc *d) {
@@ -375,15 +456,23 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
         }
     }
     hipStream_t strm = static_cast<hipStream_t>(stream);
+    if (!bf16 && s.E <= dc::kFlashMaxHeadDim && workspace_bytes < l.total) {
+        // The whole problem's deterministic partials do not fit: run it in pieces whose do.
+        st = bwd_f32_chunked(a, workspace_bytes - l.part, strm);
+        if (st != DC_OK) return st;
+        return launched(dc::launch_bwd_ref_nan(a, bf16, strm));
+    }
     if (s.E > dc::kFlashMaxHeadDim) {  // materialized over row blocks after dsum (wide.hip)
         if (dc::wide_rows(s, bf16, true, workspace_bytes - l.part) <= 0)
             return fail(DC_INVALID_ARGUMENT,
                         "flash attention backward with head_dim above 128 needs a workspace of "
                         "dc_sdpa_bwd_workspace_size bytes (at least one row of scores per kv head)");
-        return launched(dc::launch_wide_bwd(a, bf16, ws + l.part, workspace_bytes - l.part, strm));
+        st = launched(dc::launch_wide_bwd(a, bf16, ws + l.part, workspace_bytes - l.part, strm));
+    } else {
+        st = launched(bf16 ? dc::launch_bwd_bf16(a, strm) : dc::launch_bwd_f32(a, strm));
     }
-    if (!bf16) return launched(dc::launch_bwd_f32(a, strm));
-    return launched(dc::launch_bwd_bf16(a, strm));
+    if (st != DC_OK) return st;
+    return launched(dc::launch_bwd_ref_nan(a, bf16, strm));
 }
 
 }  // extern "C"
@@ -410,6 +499,7 @@ dc_status dry_run(dc_sdpa_schedule *out, F call) {
     out->deterministic = sch.deterministic;
     out->materialized_rows = sch.materialized_rows;
     out->workgroups = sch.workgroups;
+    out->chunks = sch.chunks;
     return ok();
 }
 
@@ -461,15 +551,17 @@ dc_status dc_sdpa_decode(const dc_attn_desc *d, const void *q, const void *k, co
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     if (s.E > dc::kDecodeMaxHeadDim) {  // the forward's materialized path at L = 1 (wide.hip)
         dc::FwdArgs f{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
-        return launched(dc::launch_wide_fwd(f, d->dtype == DC_BF16, workspace, workspace_bytes,
-                                            static_cast<hipStream_t>(stream)));
+        st = launched(dc::launch_wide_fwd(f, d->dtype == DC_BF16, workspace, workspace_bytes,
+                                          static_cast<hipStream_t>(stream)));
+        if (st != DC_OK) return st;
+        return launched(dc::launch_fwd_ref_rows(f, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
     }
     dc::DecodeArgs a{};
     a.s = s;
     a.q = q, a.k = k, a.v = v, a.out = out, a.lse = lse;
     a.part = static_cast<float *>(workspace);
     a.splits = dc::decode_splits(s, &a.split_len);
-    return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
+    return decode_then_ref_rows(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream));
 }
 
 dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const void *k, const void *v,
@@ -503,7 +595,7 @@ dc_status dc_sdpa_decode_noalloc(const dc_attn_desc *d, const void *q, const voi
     st = launched(dc::decode_scratch(&a.part));  // the device address, never the array's name
     if (st != DC_OK) return st;
     a.splits = dc::decode_splits(s, &a.split_len);
-    return launched(dc::launch_decode(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream)));
+    return decode_then_ref_rows(a, d->dtype == DC_BF16, static_cast<hipStream_t>(stream));
 }
 
 dc_status dc_bmm(const dc_bmm_desc *d, const float *a, const float *b, float *c, void *stream) {

@@ -274,6 +274,7 @@ struct Schedule {
     int deterministic = 1;                  // backward results identical from run to run
     int materialized_rows = 0;              // head dims above 128: rows per block (wide.hip)
     int64_t workgroups = 0;                 // workgroups of the launches, summed
+    int chunks = 1;                         // float32 backward: launch sequences (abi.hip)
 };
 inline thread_local Schedule *g_schedule = nullptr;
 

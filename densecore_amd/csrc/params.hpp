@@ -127,6 +127,14 @@ hipError_t launch_wide_fwd(const FwdArgs &a, bool bf16, void *ws, size_t bytes, 
 hipError_t launch_wide_bwd(const BwdArgs &a, bool bf16, void *ws, size_t bytes, hipStream_t st);
 constexpr int kFlashMaxHeadDim = 128;  // the flash kernels' widest instantiation
 
+// Rows the reference's blocking fixes (ref_rows.hip): causal attention with a scale that is not
+// positive, or a NaN scale.  The forward pass overwrites the rows the reference makes NaN (or 0);
+// the backward pass extends NaN rows of lse / dsum to every gradient element the reference's NaN
+// reaches.  Both launch nothing unless ref_rows_needed.
+bool ref_rows_needed(const AttnShape &s);
+hipError_t launch_fwd_ref_rows(const FwdArgs &a, bool bf16, hipStream_t st);
+hipError_t launch_bwd_ref_nan(const BwdArgs &a, bool bf16, hipStream_t st);
+
 // Compute units of the current device, and workgroups of `kernel` (`threads` per workgroup) that
 // fit on one of them; both looked up once per device (and kernel) and cached.  0 if unknown.
 int device_cus();

@@ -147,7 +147,10 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void wide_p_kernel(WideRows w) 
     const float *mrow = mask_row(w, r);
     const float lse = w.lse_in[r.bhl];
     float *x = w.x + g * S;
-    for (int key = lane; key < S; key += 64) x[key] = expf(score(w, r, mrow, key, x[key]) - lse);
+    // Causal keys past the query get 0 after the exponential, as in the reference (:363-367), so
+    // that a NaN lse leaves them 0.
+    for (int key = lane; key < S; key += 64)
+        x[key] = w.s.causal && key > r.l ? 0.f : expf(score(w, r, mrow, key, x[key]) - lse);
 }
 
 // Backward: dS = scale * P * (dP - dsum), over the dP buffer.

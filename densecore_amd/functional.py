@@ -139,7 +139,8 @@ def _matmul(x, y):
     lead = tuple(x.shape[:-2])
     if tuple(y.shape[:-2]) != lead:
         raise ValueError("bmm batch or inner dimensions mismatch")
-    out = bmm(x.reshape((-1,) + tuple(x.shape[-2:])), y.reshape((-1,) + tuple(y.shape[-2:])))
+    batch = math.prod(lead)  # explicit: reshape cannot infer -1 for tensors with no elements
+    out = bmm(x.reshape((batch,) + tuple(x.shape[-2:])), y.reshape((batch,) + tuple(y.shape[-2:])))
     return out.reshape(lead + tuple(out.shape[-2:]))
 
 

@@ -134,6 +134,10 @@ typedef struct {
     int32_t deterministic;  /* backward: 1 when dq, dk, dv are identical from run to run */
     int32_t materialized_rows; /* head_dim > 128: query rows per materialized block; 0: flash */
     int64_t workgroups;     /* workgroups of all the call's launches */
+    int32_t chunks;         /* float32 backward: pieces (whole batches, or kv heads of one batch)
+                               run one after another so that a smaller workspace still holds the
+                               deterministic partials of each; 1: the whole problem at once */
+    int32_t reserved;
 } dc_sdpa_schedule;
 
 dc_status dc_sdpa_fwd_schedule(const dc_attn_desc *d, int has_mask, size_t workspace_bytes,

@@ -17,7 +17,8 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle_sdpa.so")
+# DC_ORACLE_LIB names another build of the same source (the sanitizer build, oracle_asan.so).
+_LIB_PATH = os.environ.get("DC_ORACLE_LIB") or os.path.join(_HERE, "liboracle_sdpa.so")
 _lib = None
 
 _F = ctypes.POINTER(ctypes.c_float)

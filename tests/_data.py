@@ -75,3 +75,24 @@ def assert_bf16(got, ref, name):
     bad = ~(diff <= 1e-2 * np.abs(ref) + 1e-2 * rms)
     assert not bad.any(), (f"{name}: {int(bad.sum())} elements outside 1e-2|ref| + 1e-2 rms "
                            f"(max abs diff {float(np.nanmax(diff)):.3e}, rms {rms:.3e})")
+
+
+def _same_nans(got, ref, name):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    gn, rn = np.isnan(got), np.isnan(ref)
+    assert (gn == rn).all(), (f"{name}: NaN at {int((gn & ~rn).sum())} elements the reference has "
+                              f"finite, finite at {int((rn & ~gn).sum())} it has NaN")
+    return got[~rn], ref[~rn]
+
+
+def assert_f32_nan(got, ref, name):
+    """The reference's NaN elements exactly, and the float32 bar on every other element."""
+    g, r = _same_nans(got, ref, name)
+    assert_f32(g, r, name)
+
+
+def assert_bf16_nan(got, ref, name):
+    """The reference's NaN elements exactly, and the bf16 bar (rms over the finite elements) on
+    every other element."""
+    g, r = _same_nans(got, ref, name)
+    assert_bf16(g, r, name)

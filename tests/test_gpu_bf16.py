@@ -15,7 +15,7 @@ rows' out, lse and dq; with b = T it also gives dk and dv of every key >= a."""
 import numpy as np
 import pytest
 
-from tests._data import assert_bf16, bf16_round, make_inputs
+from tests._data import assert_bf16, assert_bf16_nan, bf16_round, make_inputs
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -66,32 +66,30 @@ def test_bf16_shapes(oracle_lib, B, H, Hkv, L, S, E, causal):
         assert_bf16(_np(a), b, name)
 
 
-@pytest.mark.parametrize("scale", [-0.4, 0.0])
+@pytest.mark.parametrize("scale", [-0.4, 0.0, float("nan")])
 @pytest.mark.parametrize("B,H,L,S,E,causal", [
-    (1, 2, 300, 300, 128, True), (2, 2, 200, 200, 64, True), (1, 2, 150, 170, 64, False),
+    (1, 2, 300, 300, 128, True), (2, 2, 200, 200, 64, True), (1, 2, 100, 300, 64, True),
+    (1, 2, 150, 170, 64, False),
 ])
 def test_bf16_negative_and_zero_scale(oracle_lib, B, H, L, S, E, causal, scale):
-    """Explicit negative and zero scales.  Causal rows are checked against the oracle with the
-    equivalent additive mask instead of its causal flag: the reference writes -inf into masked
-    scores before scaling them (-inf times a negative scale is +inf, times 0 NaN), while here
-    masked keys get probability 0 whatever the scale."""
+    """Explicit negative, zero and NaN scales give the reference's result, NaN rows included (the
+    reference scales its causal -inf fill: src/torch_attention.rs:202-216): out and lse against
+    the oracle's causal forward on the upcast inputs, the same NaN elements and the bf16 bar
+    elsewhere; the backward from the GPU's (out, lse) against the oracle's from the same."""
     from densecore_amd import _native
     rng = np.random.default_rng(L + 3 * S + 5 * E)
     q, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(2))
     k, v = (bf16_round(rng.standard_normal((B, H, S, E), dtype=np.float32)) for _ in range(2))
     print(f"[case] bf16 scale {scale} B{B} H{H} L{L} S{S} E{E} causal={causal}", flush=True)
-    full = None
-    if causal:
-        full = np.ascontiguousarray(np.broadcast_to(_offset_causal(L, S, 0), (B, H, L, S)))
-    ref_o, ref_l = oracle_lib.forward(q, k, v, False, scale, full)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, scale)
     tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
     out, lse = _native._flash_attention(tq, tk, tv, causal, scale)
-    assert_bf16(_np(out), ref_o, "out")
-    assert_bf16(_np(lse), ref_l, "lse")
-    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), False, scale, full)
+    assert_bf16_nan(_np(out), ref_o, "out")
+    assert_bf16_nan(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), causal, scale)
     got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, causal, scale)
     for name, x, y in zip(("dq", "dk", "dv"), got, ref):
-        assert_bf16(_np(x), y, name)
+        assert_bf16_nan(_np(x), y, name)
 
 
 def test_bf16_masked(oracle_lib):

@@ -25,14 +25,15 @@ def _t(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
 
 
-def _backward_poisoned(g, q, k, v, out, lse, causal, mask):
+def _backward_poisoned(g, q, k, v, out, lse, causal, mask, nbytes=None):
     from densecore_amd import _lib, _native
     dims = _native._attention_dims(q, k, v)
     B, H, Hkv, L, S, E = dims
     m, ms = _native._mask_arg(mask, dims, q.device)
     d = _native._desc(dims, causal, None, torch.float32, ms)
     L_ = _lib.lib()
-    nbytes = L_.dc_sdpa_bwd_workspace_size(d)
+    if nbytes is None:
+        nbytes = L_.dc_sdpa_bwd_workspace_size(d)
     ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=DEV)
     sched = _native._schedule(True, q, k, v, causal, mask=m, workspace_bytes=nbytes)
     runs = []
@@ -95,3 +96,61 @@ def test_f32_backward_minimum_workspace_uses_atomics():
     dsum = (8 * 2048 * 4 + 255) // 256 * 256
     assert _native._schedule(True, q, q, q, True, workspace_bytes=dsum)["deterministic"] == 0
     assert _native._schedule(True, q, q, q, True)["deterministic"] == 1
+
+
+PIECE_CASES = [  # tag, B, H, Hkv, L, S, E, causal, partial bytes after dsum, same bits as whole
+    # two pieces of 8 batches, whole tiles in each (as in the whole problem)
+    ("pieces_of_batches", 16, 16, 16, 1024, 1024, 64, True, 160 << 20, True),
+    # one batch: pieces of 44 and 20 kv heads, the second on the stream-K schedule
+    ("pieces_of_heads", 1, 64, 64, 2048, 2048, 64, True, 200 << 20, False),
+]
+
+
+@pytest.mark.parametrize("tag,B,H,Hkv,L,S,E,causal,part,same", PIECE_CASES, ids=[c[0] for c in PIECE_CASES])
+def test_f32_backward_in_pieces(oracle_lib, tag, B, H, Hkv, L, S, E, causal, part, same):
+    """A workspace that holds the deterministic partials of only part of the problem: the library
+    runs pieces of whole batches, or of one batch's kv heads, one after another, each with its own
+    fixed-order sums.  Runs are bit-identical, meet the float32 bar, and where every piece takes
+    the whole problem's schedule they equal the whole-workspace result bit for bit."""
+    from densecore_amd import _lib, _native
+    rng = np.random.default_rng(sum(map(ord, tag)) + 12)
+    q = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    k = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    v = rng.standard_normal((B, Hkv, S, E), dtype=np.float32)
+    g = rng.standard_normal((B, H, L, E), dtype=np.float32)
+    print(f"[case] f32 backward in pieces {tag} B{B} H{H} L{L} S{S} E{E}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal)
+    dsum = (B * H * L * 4 + 255) // 256 * 256
+    d = _native._desc((B, H, Hkv, L, S, E), causal, None, torch.float32, (0, 0, 0))
+    full = _lib.lib().dc_sdpa_bwd_workspace_size(d)
+    assert full > dsum + part, "the case must not fit whole"
+    t = [_t(x) for x in (g, q, k, v, ref_o, ref_l)]
+    runs, sched = _backward_poisoned(*t, causal, None, nbytes=dsum + part)
+    print(f"[schedule] {sched}", flush=True)
+    assert sched["deterministic"] == 1 and sched["chunks"] > 1, sched
+    for name, a, b, c in zip(("dq", "dk", "dv"), *runs):
+        assert torch.equal(a, b) and torch.equal(a, c), f"{tag} {name}: runs differ"
+    if same:
+        whole, wsched = _backward_poisoned(*t, causal, None)
+        assert wsched["chunks"] == 1 and wsched["deterministic"] == 1, wsched
+        for name, a, b in zip(("dq", "dk", "dv"), runs[0], whole[0]):
+            assert torch.equal(a, b), f"{tag} {name}: pieces differ from the whole problem"
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal)
+    for name, a, r in zip(("dq", "dk", "dv"), runs[0], ref):
+        assert_f32(a.cpu().numpy(), r, f"{tag} {name}")
+
+
+def test_f32_backward_workspace_bound():
+    """The Python boundary passes at most max(DETERMINISTIC_WORKSPACE_BYTES, 8 |dq|) to the float32
+    backward: at B1 H32 L=S=8192 E128 causal (about 4 GiB of slots) the call still runs in pieces
+    with fixed-order sums instead of allocating them all."""
+    from densecore_amd import _lib, _native
+    dims = (1, 32, 32, 8192, 8192, 128)
+    d = _native._desc(dims, True, None, torch.float32, (0, 0, 0))
+    L_ = _lib.lib()
+    full = L_.dc_sdpa_bwd_workspace_size(d)
+    used = _native._bwd_workspace_bytes(L_, d, dims, torch.float32)
+    assert full > 3 << 30 and used == max(_native.DETERMINISTIC_WORKSPACE_BYTES, 8 * 32 * 8192 * 128 * 4)
+    q = torch.empty((1, 32, 8192, 128), device=DEV)
+    sched = _native._schedule(True, q, q, q, True)
+    assert sched["deterministic"] == 1 and sched["chunks"] > 1, sched

@@ -224,3 +224,35 @@ def test_multi_head_attention_batch_first_and_no_weights():
     mod.batch_first = False
     ref, _ = mod(_t(x).transpose(0, 1), _t(x).transpose(0, 1), _t(x).transpose(0, 1))
     assert_f32(_np(out), _np(ref.transpose(0, 1)), "batch_first")
+
+
+@pytest.mark.parametrize("shape", [
+    ((0, 2, 5, 4), (0, 2, 6, 4), (0, 2, 6, 3)),   # B = 0
+    ((2, 3, 0, 4), (2, 3, 6, 4), (2, 3, 6, 3)),   # L = 0
+    ((2, 3, 5, 0), (2, 3, 6, 0), (2, 3, 6, 3)),   # E = 0: scores are 0, out = mean of v
+    ((2, 5, 0), (2, 7, 0), (2, 7, 4)),            # rank 3, E = 0
+])
+@pytest.mark.parametrize("causal", [False, True])
+def test_math_path_empty_dims(shape, causal):
+    """Shapes with a zero length, batch or head dim go to the math path (the reference's flash
+    predicate needs L, S and E non-zero, functional.py:310-312), and its products accept them:
+    out has the query's leading shape and v's last dim; with E = 0 every score is 0, so out is the
+    mean of v over the keys each row sees, and the gradients follow."""
+    from densecore_amd import functional as F
+    qs, ks, vs = shape
+    print(f"[case] math path empty dims q{qs} k{ks} v{vs} causal={causal}", flush=True)
+    q, k, v = (RNG.standard_normal(s).astype(np.float32) for s in (qs, ks, vs))
+    tq, tk, tv = _t(q, True), _t(k, True), _t(v, True)
+    out = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal)
+    assert tuple(out.shape) == qs[:-1] + vs[-1:]
+    L, S = qs[-2], ks[-2]
+    allowed = np.tril(np.ones((L, S), bool)) if causal else np.ones((L, S), bool)
+    w = allowed / np.maximum(allowed.sum(-1, keepdims=True), 1)
+    if qs[-1] == 0 and out.numel():
+        assert_f32(_np(out), np.matmul(w, v).astype(np.float32), "E = 0 out")
+    g = RNG.standard_normal(tuple(out.shape)).astype(np.float32)
+    out.backward(_t(g))
+    for t, s in ((tq, qs), (tk, ks), (tv, vs)):
+        assert t.grad is not None and tuple(t.grad.shape) == s
+    if qs[-1] == 0 and out.numel():
+        assert_f32(_np(tv.grad), np.matmul(np.swapaxes(w, -1, -2), g).astype(np.float32), "E = 0 dv")

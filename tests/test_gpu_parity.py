@@ -11,7 +11,7 @@ fully masked rows, one key, grouped heads).
 import numpy as np
 import pytest
 
-from tests._data import additive, assert_f32
+from tests._data import additive, assert_f32, assert_f32_nan
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -197,38 +197,46 @@ def test_grouped_heads(oracle_lib, B, H, Hkv, L, S, E, causal):
     _check(oracle_lib, q, k, v, g, causal, tag="gqa")
 
 
-@pytest.mark.parametrize("scale", [-0.4, 0.0])
-@pytest.mark.parametrize("B,H,L,S,E,causal", [
-    (2, 2, 100, 100, 64, True),   # one-wave forward
-    (1, 3, 300, 300, 64, True),   # 4-wave forward
-    (1, 2, 600, 600, 64, True),   # split key ranges
-    (1, 2, 200, 300, 32, False),  # 64-key tiles
+@pytest.mark.parametrize("scale", [-0.4, 0.0, -0.0, float("nan")])
+@pytest.mark.parametrize("B,H,L,S,E,causal,masked", [
+    (2, 2, 100, 100, 64, True, False),    # one-wave forward
+    (1, 3, 300, 300, 64, True, False),    # 4-wave forward
+    (1, 2, 600, 600, 64, True, False),    # split key ranges
+    (1, 1, 1100, 1100, 32, True, False),  # q blocks of 256, two key blocks of 512
+    (1, 2, 100, 300, 64, True, False),    # L < S: keys no query sees
+    (1, 2, 300, 100, 64, True, False),    # L > S
+    (1, 1, 3, 3, 16, True, False),        # one block narrower than 4 keys
+    (1, 2, 150, 150, 64, True, True),     # a float mask as well
+    (1, 2, 130, 130, 160, True, False),   # head dim above 128 (materialized rows)
+    (1, 2, 200, 300, 32, False, False),   # non-causal: only a NaN scale changes anything
 ])
-def test_negative_and_zero_scale(oracle_lib, B, H, L, S, E, causal, scale):
-    """A scale passed explicitly may be negative or zero (the reference takes any float): without
-    a mask the forward applies the scale after the tile max, with negated queries for a negative
-    one, and treats zero as the smallest normal float.  Causal rows are checked against the
-    oracle without causal masking and with the equivalent additive mask: the reference writes
-    -inf into masked scores before scaling them, so a negative or zero scale makes its causal rows
-    NaN (-inf times -0.4 is +inf, times 0 is NaN), while here, as in PyTorch, masked keys get
-    probability 0 whatever the scale."""
+def test_negative_and_zero_scale(oracle_lib, B, H, L, S, E, causal, masked, scale):
+    """An explicit scale may be negative, zero or NaN (the reference takes any float), and the
+    result is the reference's, NaN rows included: it writes -inf into causally masked scores
+    before it scales them (src/torch_attention.rs:202-216), so -inf times a negative scale is
+    +inf and times 0 NaN, and every row with such a score in its last key block comes out NaN;
+    a NaN scale makes every row NaN (0 without a mask when the only block is narrower than 4
+    keys).  torch's CPU SDPA gives the same rows.  Out and lse are compared with the oracle's
+    causal forward on the same inputs: the same NaN elements, the float32 bar elsewhere; the
+    backward from the oracle's (out, lse) must spread those NaN to the same gradient elements."""
     rng = np.random.default_rng(B + 3 * H + 5 * L + 7 * S + 11 * E)
     q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
     k, v = (rng.standard_normal((B, H, S, E), dtype=np.float32) for _ in range(2))
-    if not causal:
-        _check(oracle_lib, q, k, v, g, False, scale, tag=f"scale {scale}")
-        return
-    print(f"[case] causal scale {scale} q{q.shape}", flush=True)
-    tri = np.where(np.arange(S)[None, :] <= np.arange(L)[:, None], 0.0, -np.inf).astype(np.float32)
-    full = np.ascontiguousarray(np.broadcast_to(tri, (B, H, L, S)))
-    ref_o, ref_l = oracle_lib.forward(q, k, v, False, scale, full)
-    out, lse = _run_fwd(q, k, v, True, scale, None)
-    assert_f32(out, ref_o, f"causal scale {scale} out")
-    assert_f32(lse, ref_l, f"causal scale {scale} lse")
-    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, False, scale, full)
-    got = _run_bwd(g, q, k, v, ref_o, ref_l, True, scale, None)
+    mask = None
+    if masked:
+        mask = rng.standard_normal((B, H, L, S)).astype(np.float32)
+        mask[rng.random((B, H, L, S)) < 0.2] = -np.inf
+    print(f"[case] scale {scale} q{q.shape} k{k.shape} causal={causal} mask={masked}", flush=True)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, scale, mask)
+    out, lse = _run_fwd(q, k, v, causal, scale, mask)
+    assert_f32_nan(out, ref_o, f"scale {scale} out")
+    assert_f32_nan(lse, ref_l, f"scale {scale} lse")
+    if causal and scale == scale and (S >= 4 or masked):
+        assert bool(np.isnan(ref_l).any()), "the case must be one the reference makes NaN"
+    ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal, scale, mask)
+    got = _run_bwd(g, q, k, v, ref_o, ref_l, causal, scale, mask)
     for name, x, y in zip(("dq", "dk", "dv"), got, ref):
-        assert_f32(x, y, f"causal scale {scale} {name}")
+        assert_f32_nan(x, y, f"scale {scale} {name}")
 
 
 @pytest.mark.parametrize("B,H,L,S,E,causal", [

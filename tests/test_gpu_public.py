@@ -24,7 +24,7 @@ the math path, its batched products (``dc_bmm``) and the device BLAS (``torch.ma
 import numpy as np
 import pytest
 
-from tests._data import assert_bf16, assert_f32, bf16_round
+from tests._data import assert_bf16, assert_bf16_nan, assert_f32, assert_f32_nan, bf16_round
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -45,6 +45,12 @@ def flash_only(monkeypatch):
     monkeypatch.setattr(torch, "matmul", boom)
     monkeypatch.setattr(torch, "bmm", boom)
     return F
+
+
+def _same_bits(a, b):
+    """Equal element by element, NaN matching NaN (the reference's NaN rows)."""
+    return a.shape == b.shape and bool(torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a.view(torch.int32),
+                                                  b.view(torch.int16) if b.dtype == torch.bfloat16 else b.view(torch.int32)))
 
 
 def _leaf(x, dtype):
@@ -100,6 +106,9 @@ CASES = [  # tag, B, H, Hkv, L, S, E, causal, mask kind, scale, gqa
     ("float2d", 2, 2, 2, 33, 65, 16, False, "float2d", None, False),
     ("gqa_causal", 2, 8, 2, 130, 130, 64, True, None, None, True),
     ("gqa_padding", 2, 6, 3, 64, 150, 128, False, "bool4d_padding", 0.3, True),
+    # the reference scales its causal -inf fill: NaN rows (src/torch_attention.rs:202-216)
+    ("causal_negative_scale", 1, 2, 2, 100, 100, 64, True, None, -0.4, False),
+    ("causal_zero_scale", 2, 2, 2, 300, 300, 32, True, None, 0.0, False),
 ]
 
 
@@ -134,7 +143,7 @@ def test_public_flash_autograd(oracle_lib, flash_only, dtype, tag, B, H, Hkv, L,
         m = None if add_mask is None else torch.from_numpy(add_mask).to(DEV)
         o_gpu, l_gpu = _native._flash_attention(*(torch.from_numpy(x).to(DEV, tdt) for x in (q, k, v)),
                                                 causal, scale, m)
-        assert torch.equal(o_gpu, out.detach()), "bf16 forward is not deterministic"
+        assert _same_bits(o_gpu, out.detach()), "bf16 forward is not deterministic"
         ref_o, ref_l, ref = _reference(oracle_lib, q, kw_, vw_, g, causal, scale, add_mask,
                                        o_gpu.float().cpu().numpy(), l_gpu.cpu().numpy())
     else:
@@ -144,6 +153,9 @@ def test_public_flash_autograd(oracle_lib, flash_only, dtype, tag, B, H, Hkv, L,
         rdk = rdk.reshape(B, Hkv, rep, S, E).sum(axis=2)
         rdv = rdv.reshape(B, Hkv, rep, S, E).sum(axis=2)
     check = assert_bf16 if bf16 else assert_f32
+    if scale is not None and not scale > 0:
+        check = assert_bf16_nan if bf16 else assert_f32_nan
+        assert np.isnan(ref_o).any()
     check(out.detach().float().cpu().numpy(), ref_o, f"{tag} out")
     for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         check(a, b, f"{tag} {name}")
@@ -170,3 +182,41 @@ def test_public_bool_mask_stays_on_device(flash_only):
     assert fm.device.type == "cuda" and fm.dtype == torch.float32 and tuple(fm.shape) == (2, 4, 5, 3)
     assert fm.stride()[:3] == (0, 0, 0)
     assert fm[1, 3, 4].tolist() == [0.0, float("-inf"), 0.0]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,T,H,D", [(2, 96, 4, 32), (3, 257, 6, 64), (1, 130, 2, 128)])
+def test_public_transposed_views(oracle_lib, flash_only, dtype, B, T, H, D):
+    """The reference's own consumer (examples/tiny_gpt.py:30-38) hands attention (B, T, H, D)
+    projections viewed as (B, H, T, D) through .transpose(1, 2), is_causal=True.  The same views
+    here, with autograd back to the (B, T, H * D) leaves: out and the leaves' gradients against the
+    oracle on the contiguous (B, H, T, D) copies."""
+    bf16 = dtype == "bf16"
+    tdt = torch.bfloat16 if bf16 else torch.float32
+    rng = np.random.default_rng(B * 1000 + T + H * D + (7 if bf16 else 0))
+    x = [rng.standard_normal((B, T, H * D), dtype=np.float32) for _ in range(3)]
+    g = rng.standard_normal((B, H, T, D), dtype=np.float32)
+    if bf16:
+        x, g = [bf16_round(a) for a in x], bf16_round(g)
+    print(f"[case] public {dtype} transposed views B{B} T{T} H{H} D{D}", flush=True)
+    leaves = [_leaf(a, tdt) for a in x]
+    q, k, v = (t.reshape(B, T, H, D).transpose(1, 2) for t in leaves)
+    assert not q.is_contiguous()
+    out = flash_only.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert type(out.grad_fn).__name__ == "_FlashAttentionBackward", type(out.grad_fn).__name__
+    out.backward(torch.from_numpy(g).to(DEV, tdt))
+    torch.cuda.synchronize()
+    qn, kn, vn = (np.ascontiguousarray(a.reshape(B, T, H, D).transpose(0, 2, 1, 3)) for a in x)
+    if bf16:
+        from densecore_amd import _native
+        o_gpu, l_gpu = _native._flash_attention(*(torch.from_numpy(a).to(DEV, tdt) for a in (qn, kn, vn)), True)
+        assert _same_bits(o_gpu, out.detach()), "bf16 forward differs on a transposed view"
+        ref_o, _, ref = _reference(oracle_lib, qn, kn, vn, g, True, None, None,
+                                   o_gpu.float().cpu().numpy(), l_gpu.cpu().numpy())
+    else:
+        ref_o, _, ref = _reference(oracle_lib, qn, kn, vn, g, True, None, None)
+    check = assert_bf16 if bf16 else assert_f32
+    check(out.detach().float().cpu().numpy(), ref_o, "transposed out")
+    for name, leaf, r in zip(("dq", "dk", "dv"), leaves, ref):
+        got = leaf.grad.float().cpu().numpy().reshape(B, T, H, D).transpose(0, 2, 1, 3)
+        check(got, r, f"transposed {name}")

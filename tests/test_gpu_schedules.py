@@ -14,8 +14,10 @@ over their key tiles, each piece writing float32 partials that a reduction sums 
 Backward (float32): the backward either gives each key tile (128 keys of one kv head) to one workgroup, or, when
 whole tiles would leave part of the device idle (fewer tiles than resident workgroups, or a
 ragged last wave of equal non-causal tiles), cuts the steps of all tiles into equal ranges, one
-per resident workgroup (stream-K).  A tile cut between ranges adds its dK / dV atomically into rows the pre-kernel
-cleared; tiles without steps (causal keys past the last query) are cleared there too.  These
+per resident workgroup (stream-K).  A tile cut between ranges leaves each range's dK / dV share in a slot
+of the workspace, summed in range order by a reduction (with only dsum in the workspace, the
+shares are added atomically into rows the pre-kernel cleared; tiles without steps, causal keys
+past the last query, are cleared there too).  These
 cases call the C ABI with dQ, dK and dV pre-filled with NaN, so a row neither schedule writes
 fails.  On MI355X (256 CUs) the shapes marked "whole" take the one-tile-per-workgroup grid, the
 others stream-K.  Tolerance, as for every float32 output: |gpu - ref| <= 2e-5 + 1e-5 |ref|.
