@@ -7,6 +7,7 @@ Hand-written HIP kernels for gfx950 (``csrc/``) behind the C ABI in ``include/dc
 """
 from . import functional  # noqa: F401
 from . import nn, random  # noqa: F401
-from ._native import _flash_attention, _flash_attention_backward, _flash_decode  # noqa: F401
+from ._native import _flash_attention, _flash_attention_backward, _flash_decode, consistent_scores  # noqa: F401
 
-__all__ = ["functional", "nn", "random", "_flash_attention", "_flash_attention_backward", "_flash_decode"]
+__all__ = ["functional", "nn", "random", "_flash_attention", "_flash_attention_backward", "_flash_decode",
+           "consistent_scores"]

@@ -11,6 +11,7 @@ LIB_PATH = os.path.join(_HERE, "libdcattn.so")
 
 DC_OK, DC_INVALID_ARGUMENT, DC_UNSUPPORTED, DC_EXECUTION_FAILED = 0, 1, 2, 3
 DC_F32, DC_BF16 = 0, 1
+DC_FLAG_CONSISTENT_SCORES = 1
 
 # Every symbol include/dc_attn.h and include/dc_math.h declare.
 EXPORTS = ("dc_abi_version", "dc_last_error",
@@ -29,7 +30,7 @@ class Desc(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("heads", ctypes.c_int64), ("kv_heads", ctypes.c_int64),
                 ("q_len", ctypes.c_int64), ("kv_len", ctypes.c_int64), ("head_dim", ctypes.c_int64),
                 ("causal", ctypes.c_int32), ("has_scale", ctypes.c_int32), ("scale", ctypes.c_double),
-                ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("flags", ctypes.c_int32),
                 ("mask_stride_b", ctypes.c_int64), ("mask_stride_h", ctypes.c_int64),
                 ("mask_stride_l", ctypes.c_int64)]
 

@@ -65,10 +65,26 @@ def _mask_arg(mask, dims, dev):
     return mask, (mask.stride(0), mask.stride(1), mask.stride(2))
 
 
+# DC_FLAG_CONSISTENT_SCORES on every call when set (include/dc_attn.h): the float32 backward at
+# head dims 65-128 forms its scores in the forward's order of products, so that exp(score - lse)
+# normalizes exactly as the forward's did (slower); see consistent_scores().
+CONSISTENT_SCORES = False
+
+
+def consistent_scores(enabled=True):
+    """Make the float32 backward at head dims 65-128 form its scores in the forward's order
+    (``DC_FLAG_CONSISTENT_SCORES``) for the calls that follow, or go back to the faster 8-wave
+    tile.  Head dims up to 64 always use the forward's order.  Returns the previous setting."""
+    global CONSISTENT_SCORES
+    previous, CONSISTENT_SCORES = CONSISTENT_SCORES, bool(enabled)
+    return previous
+
+
 def _desc(dims, causal, scale, dtype, mstrides):
     B, H, Hkv, L, S, E = dims
+    flags = _lib.DC_FLAG_CONSISTENT_SCORES if CONSISTENT_SCORES else 0
     return _lib.Desc(B, H, Hkv, L, S, E, int(bool(causal)), int(scale is not None),
-                     float(scale) if scale is not None else 0.0, _DTYPES[dtype], 0, *mstrides)
+                     float(scale) if scale is not None else 0.0, _DTYPES[dtype], flags, *mstrides)
 
 
 def _ptr(t):

@@ -89,6 +89,8 @@ dc_status check_dims(const dc_attn_desc *d, dc::AttnShape *s) {
         return fail(DC_INVALID_ARGUMENT, "flash attention q/k/v shapes do not match");
     if (d->dtype != DC_F32 && d->dtype != DC_BF16)
         return fail(DC_INVALID_ARGUMENT, "flash attention dtype must be float32 or bfloat16");
+    if ((d->flags & ~DC_FLAG_CONSISTENT_SCORES) != 0)
+        return fail(DC_INVALID_ARGUMENT, "flash attention flags has unknown bits");
     for (int64_t x : dims)
         if (x > INT32_MAX)
             return fail(DC_UNSUPPORTED, "flash attention dimension exceeds 2^31 - 1");
@@ -108,6 +110,7 @@ dc_status check_dims(const dc_attn_desc *d, dc::AttnShape *s) {
     s->mask = nullptr;
     s->msb = s->msh = s->msl = 0;
     s->vec = true;
+    s->consistent = (d->flags & DC_FLAG_CONSISTENT_SCORES) != 0;
     return ok();
 }
 

@@ -59,11 +59,16 @@ struct alignas(16) BwdSmem {
 
 // Threads of a backward workgroup: 8 waves of 16 keys at D = 128 (key_tile16), 4 waves of 32 keys
 // otherwise (key_tile).
+// At D = 128 a caller may ask for the forward's score order instead (AttnShape::consistent): the
+// 4-wave tile, one wave per SIMD.
 constexpr bool kSixteenKeys(int D) { return D == 128; }
-constexpr int bwd_threads(int D) { return kSixteenKeys(D) ? 2 * kThreads : kThreads; }
-// Waves per SIMD the kernels are built for: D = 128 two (one 8-wave workgroup per CU); below,
-// two without a mask (two 4-wave workgroups), one with.
-constexpr int bwd_waves_per_eu(int D, bool mask) { return D == 128 ? 2 : (mask ? 1 : 2); }
+constexpr int layout_threads(bool k16) { return k16 ? 2 * kThreads : kThreads; }
+constexpr int bwd_threads(int D) { return layout_threads(kSixteenKeys(D)); }
+// Waves per SIMD the kernels are built for: the 8-wave tile two (one workgroup per CU); the 4-wave
+// tile at D = 128 one; below, two without a mask (two 4-wave workgroups), one with.
+constexpr int bwd_waves_per_eu(int D, bool mask, bool k16) {
+    return k16 ? 2 : (D == 128 ? 1 : (mask ? 1 : 2));
+}
 
 // Register staging of one step's Q and dO rows (fast path: E == D, 16-byte aligned).
 template <int D, int NT = bwd_threads(D)>
@@ -118,10 +123,10 @@ struct QStage {
 };
 
 // Generic path (any E <= D, any alignment): straight into LDS.
-template <int D>
+template <int D, int NT>
 DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const float *lseb,
                         const float *dsumb, int m0, int L, int E, int tid) {
-    for (int i = tid; i < kBM * D; i += bwd_threads(D)) {
+    for (int i = tid; i < kBM * D; i += NT) {
         const int r = i / D, c = i % D, qq = m0 + r;
         const bool ok = qq < L && c < E;
         sm.q[r][c] = ok ? qb[(int64_t)qq * E + c] : 0.f;
@@ -146,10 +151,10 @@ DEVI void stage_generic(BwdSmem<D> &sm, const float *qb, const float *gb, const 
 // 16 kb + 4 (l/16) + u, and its dS and K^T operands for the block are one ds_read_b128 each.
 // Keys are covered in whole blocks up to nkeys rounded up to 16; the extra keys lie in the
 // same 32-key wave group as key nkeys - 1, whose dS columns this step wrote (zeros past S).
-template <int D>
+template <int D, int NT>
 DEVI void dq_product(const BwdSmem<D> &sm, float *dst, bool atomic, int nrows, int nkeys, int E,
                      float scale, int wave, int lane) {
-    constexpr int WH = bwd_threads(D) / 128;  // waves per 16-query half (the D dims split WH ways)
+    constexpr int WH = NT / 128;  // waves per 16-query half (the D dims split WH ways)
     constexpr int TPW = D / (16 * WH);
     constexpr int NB = kBN / 16;  // 16-key blocks in a full tile
     const int r16 = lane & 15, c4 = lane >> 4;
@@ -339,7 +344,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         return a.dq_part + (slot0 + (int64_t)bh * (s.L - rf) + (m0 - rf)) * s.E;
     };
 
-    QStage<D> stage;
+    QStage<D, kThreads> stage;
     if (VEC && i0 < i1) {
         const int bh = step_head(i0);
         stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
@@ -351,12 +356,12 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
         __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
         if (prev_bh >= 0)
-            dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
+            dq_product<D, kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
                           s.scale, wave, lane);
         if (VEC) {
             stage.store(sm, tid);
         } else {
-            stage_generic<D>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
+            stage_generic<D, kThreads>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
                              static_cast<const float *>(a.dout) + (int64_t)bh * s.L * s.E,
                              a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
         }
@@ -433,7 +438,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     }
     __syncthreads();
     if (prev_bh >= 0)
-        dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
+        dq_product<D, kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
                       wave, lane);
 
     if (kv_atomic) {
@@ -514,7 +519,7 @@ template <int D, bool CAUSAL, bool MASK, bool VEC>
 DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
                      float *vdst, bool kv_atomic) {
     static_assert(kSixteenKeys(D), "the 8-wave tile is for head dim 128");
-    constexpr int NT = bwd_threads(D), NKB = D / 16;
+    constexpr int NT = 2 * kThreads, NKB = D / 16;
 
     const AttnShape &s = a.s;
     const int wave = tid >> 6, lane = tid & 63, r16 = lane & 15, c4 = lane >> 4;
@@ -573,7 +578,7 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         return a.dq_part + (slot0 + (int64_t)bh * (s.L - rf) + (m0 - rf)) * s.E;
     };
 
-    QStage<D> stage;
+    QStage<D, 2 * kThreads> stage;
     if (VEC && i0 < i1) {
         const int bh = step_head(i0);
         stage.load(static_cast<const float *>(a.q) + (int64_t)bh * s.L * D,
@@ -585,12 +590,12 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         const int bh = step_head(i), h = bh - b * s.H, m0 = step_m0(i);
         __syncthreads();  // the previous step's S/dP/dV/dK readers and dS writers are done
         if (prev_bh >= 0)
-            dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
+            dq_product<D, 2 * kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E,
                           s.scale, wave, lane);
         if (VEC) {
             stage.store(sm, tid);
         } else {
-            stage_generic<D>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
+            stage_generic<D, 2 * kThreads>(sm, static_cast<const float *>(a.q) + (int64_t)bh * s.L * s.E,
                              static_cast<const float *>(a.dout) + (int64_t)bh * s.L * s.E,
                              a.lse + (int64_t)bh * s.L, a.dsum + (int64_t)bh * s.L, m0, s.L, s.E, tid);
         }
@@ -701,7 +706,7 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
     }
     __syncthreads();
     if (prev_bh >= 0)
-        dq_product<D>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
+        dq_product<D, 2 * kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
                       wave, lane);
 
     if (kv_atomic) {
@@ -752,23 +757,23 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
 }
 
 // The key tile of either layout.
-template <int D, bool CAUSAL, bool MASK, bool VEC>
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool K16>
 DEVI void key_tile_any(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, int i0, int i1, float *kdst,
                        float *vdst, bool kv_atomic) {
-    if constexpr (kSixteenKeys(D))
+    if constexpr (K16)
         key_tile16<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
     else
         key_tile<D, CAUSAL, MASK, VEC>(a, sm, tid, bhk, kt, i0, i1, kdst, vdst, kv_atomic);
 }
 
-template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK), bwd_waves_per_eu(D, MASK)))) void bwd_f32_kernel(BwdArgs a) {
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool K16 = kSixteenKeys(D)>
+__global__ __launch_bounds__(layout_threads(K16)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK, K16), bwd_waves_per_eu(D, MASK, K16)))) void bwd_f32_kernel(BwdArgs a) {
     __shared__ BwdSmem<D> sm;
     const int BHk = a.s.B * a.s.Hkv;
     const int kt = blockIdx.x / BHk;  // tile 0 has the most causal work, so it goes first
     const int bhk = blockIdx.x % BHk;
     const int64_t row0 = ((int64_t)bhk * a.s.S + (int64_t)kt * kBN) * a.s.E;
-    key_tile_any<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, 0, tile_steps(a.s, kt),
+    key_tile_any<D, CAUSAL, MASK, VEC, K16>(a, sm, threadIdx.x, bhk, kt, 0, tile_steps(a.s, kt),
                                    static_cast<float *>(a.dk) + row0, static_cast<float *>(a.dv) + row0, false);
 }
 
@@ -782,8 +787,8 @@ DEVI float *kv_slot(const BwdArgs &a, int64_t range, int which) {
 // One workgroup per range of the stream-K schedule, ranges dealt to the 8 XCDs in contiguous
 // blocks (workgroup w runs on XCD w % 8), so the key tiles of one kv head, which read the same
 // Q / dO, share an L2.
-template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK), bwd_waves_per_eu(D, MASK)))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
+template <int D, bool CAUSAL, bool MASK, bool VEC, bool K16 = kSixteenKeys(D)>
+__global__ __launch_bounds__(layout_threads(K16)) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu(D, MASK, K16), bwd_waves_per_eu(D, MASK, K16)))) void bwd_f32_streamk_kernel(BwdArgs a, StreamK sk) {
     __shared__ BwdSmem<D> sm;
     const int w = blockIdx.x;
     const int64_t c = (int64_t)(w & 7) * (sk.chunks >> 3) + (w >> 3);
@@ -811,7 +816,7 @@ __global__ __launch_bounds__(bwd_threads(D)) __attribute__((amdgpu_waves_per_eu(
             kd = kv_slot(a, c, first ? 0 : 1);
             vd = kd + (int64_t)kBN * a.s.E;
         }
-        key_tile_any<D, CAUSAL, MASK, VEC>(a, sm, threadIdx.x, bhk, kt, i, i1, kd, vd, !whole && !a.kv_part);
+        key_tile_any<D, CAUSAL, MASK, VEC, K16>(a, sm, threadIdx.x, bhk, kt, i, i1, kd, vd, !whole && !a.kv_part);
         first = false;
         pos += i1 - i;
         i = 0;
@@ -991,22 +996,22 @@ size_t dq_part_bytes(const AttnShape &s) {
 size_t kv_part_bytes(const StreamK &sk, int E) { return (size_t)sk.chunks * 4 * kBN * E * sizeof(float); }
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-template <int D, bool VEC>
+template <int D, bool VEC, bool K16>
 hipError_t launch_dv(const BwdArgs &a, const StreamK &sk, hipStream_t st) {
     const bool mask = a.s.mask != nullptr;
     if (sk.chunks > 0) {
-        const dim3 grid(sk.chunks), block(bwd_threads(D));
-        if (a.s.causal && mask) return launch(bwd_f32_streamk_kernel<D, true, true, VEC>, grid, block, st, a, sk);
-        if (a.s.causal) return launch(bwd_f32_streamk_kernel<D, true, false, VEC>, grid, block, st, a, sk);
-        if (mask) return launch(bwd_f32_streamk_kernel<D, false, true, VEC>, grid, block, st, a, sk);
-        return launch(bwd_f32_streamk_kernel<D, false, false, VEC>, grid, block, st, a, sk);
+        const dim3 grid(sk.chunks), block(layout_threads(K16));
+        if (a.s.causal && mask) return launch(bwd_f32_streamk_kernel<D, true, true, VEC, K16>, grid, block, st, a, sk);
+        if (a.s.causal) return launch(bwd_f32_streamk_kernel<D, true, false, VEC, K16>, grid, block, st, a, sk);
+        if (mask) return launch(bwd_f32_streamk_kernel<D, false, true, VEC, K16>, grid, block, st, a, sk);
+        return launch(bwd_f32_streamk_kernel<D, false, false, VEC, K16>, grid, block, st, a, sk);
     }
     const int nkt = (a.s.S + kBN - 1) / kBN;
-    const dim3 grid(nkt * a.s.B * a.s.Hkv), block(bwd_threads(D));
-    if (a.s.causal && mask) return launch(bwd_f32_kernel<D, true, true, VEC>, grid, block, st, a);
-    if (a.s.causal) return launch(bwd_f32_kernel<D, true, false, VEC>, grid, block, st, a);
-    if (mask) return launch(bwd_f32_kernel<D, false, true, VEC>, grid, block, st, a);
-    return launch(bwd_f32_kernel<D, false, false, VEC>, grid, block, st, a);
+    const dim3 grid(nkt * a.s.B * a.s.Hkv), block(layout_threads(K16));
+    if (a.s.causal && mask) return launch(bwd_f32_kernel<D, true, true, VEC, K16>, grid, block, st, a);
+    if (a.s.causal) return launch(bwd_f32_kernel<D, true, false, VEC, K16>, grid, block, st, a);
+    if (mask) return launch(bwd_f32_kernel<D, false, true, VEC, K16>, grid, block, st, a);
+    return launch(bwd_f32_kernel<D, false, false, VEC, K16>, grid, block, st, a);
 }
 
 template <int D>
@@ -1030,7 +1035,12 @@ hipError_t launch_d(const BwdArgs &args, size_t part_bytes, hipStream_t st) {
     if (rows_blocks + zero_blocks > 0)
         return_if(launch(bwd_pre_f32_kernel, dim3((unsigned)(rows_blocks + zero_blocks)), dim3(256), st, a, sk,
                          rows_blocks));
-    return_if((a.s.vec ? launch_dv<D, true>(a, sk, st) : launch_dv<D, false>(a, sk, st)));
+    // D = 128: the 8-wave tile of 16 keys, or on request the forward-consistent 4-wave tile.
+    if (D == 128 && a.s.consistent)
+        return_if((a.s.vec ? launch_dv<D, true, false>(a, sk, st) : launch_dv<D, false, false>(a, sk, st)));
+    else
+        return_if((a.s.vec ? launch_dv<D, true, kSixteenKeys(D)>(a, sk, st)
+                           : launch_dv<D, false, kSixteenKeys(D)>(a, sk, st)));
     if (!a.dq_part) return hipSuccess;
     const int64_t dq_threads = rows * ((a.s.E + 3) / 4);
     const int dq_blocks = (int)((dq_threads + 255) / 256);

@@ -16,6 +16,7 @@ struct AttnShape {
     const float *mask; // additive, or nullptr
     int64_t msb, msh, msl;
     bool vec;          // E equals the kernel's padded head dim and pointers are 16-byte aligned
+    bool consistent;   // DC_FLAG_CONSISTENT_SCORES: float32 backward scores in the forward's order
 };
 
 struct FwdArgs {

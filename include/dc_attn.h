@@ -60,9 +60,19 @@ typedef struct {
     int32_t has_scale; /* 0: scale = 1/sqrt(head_dim), computed in double then rounded */
     double scale;
     int32_t dtype;     /* dc_dtype of q, k, v, out, grad_out, dq, dk, dv (lse is float32) */
-    int32_t reserved;
+    int32_t flags;     /* DC_FLAG_* bits; 0 for the defaults */
     int64_t mask_stride_b, mask_stride_h, mask_stride_l; /* elements; used when mask != NULL */
 } dc_attn_desc;
+
+/* dc_attn_desc.flags.  DC_FLAG_CONSISTENT_SCORES (float32 backward, head dims 65-128): form the
+ * scores q.k in the forward's order of products (v_mfma_f32_32x32x2_f32 with the forward's pairing
+ * of dims, 32 keys per wave), so that exp(score - lse) normalizes exactly as the forward's did.
+ * Without it these head dims take an 8-wave tile of 16 keys on 16x16x4 products (about 20% faster
+ * on few-heads shapes), whose scores round in another order: at ordinary scores the results are the
+ * same to the float32 bar, at scores near 100 the gradients' error against exact arithmetic grows
+ * to a few times the reference's.  No effect elsewhere (head dims up to 64 always use the
+ * forward's order).  Other bits are reserved and must be 0. */
+#define DC_FLAG_CONSISTENT_SCORES 1
 
 /* Version of this ABI (bumped on any incompatible change). */
 int dc_abi_version(void);

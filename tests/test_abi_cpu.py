@@ -42,6 +42,7 @@ def test_descriptor_layout_matches_header(tmp_path):
                    "int main(void){printf(\"%zu %zu %zu %zu %zu\\n\", sizeof(dc_attn_desc),"
                    " offsetof(dc_attn_desc, causal), offsetof(dc_attn_desc, scale),"
                    " offsetof(dc_attn_desc, dtype), offsetof(dc_attn_desc, mask_stride_l));"
+                   "printf(\"%zu %d\\n\", offsetof(dc_attn_desc, flags), DC_FLAG_CONSISTENT_SCORES);"
                    "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
@@ -49,7 +50,7 @@ def test_descriptor_layout_matches_header(tmp_path):
                                        check=True).stdout.split()))
     D = _lib.Desc
     assert got == [ctypes.sizeof(D), D.causal.offset, D.scale.offset, D.dtype.offset,
-                   D.mask_stride_l.offset]
+                   D.mask_stride_l.offset, D.flags.offset, _lib.DC_FLAG_CONSISTENT_SCORES]
 
 
 def test_softmax_descriptor_layout_matches_header(tmp_path):
@@ -99,7 +100,7 @@ def test_softmax_empty_rows_accepted():
 
 def desc(**kw):
     d = dict(batch=2, heads=4, kv_heads=2, q_len=8, kv_len=8, head_dim=16, causal=0, has_scale=0,
-             scale=0.0, dtype=_lib.DC_F32, reserved=0, mask_stride_b=0, mask_stride_h=0,
+             scale=0.0, dtype=_lib.DC_F32, flags=0, mask_stride_b=0, mask_stride_h=0,
              mask_stride_l=0)
     d.update(kw)
     return _lib.Desc(**d)
@@ -115,6 +116,7 @@ def fwd(d, mask=None):
     (dict(kv_heads=0), _lib.DC_INVALID_ARGUMENT, "q/k/v shapes do not match"),
     (dict(q_len=-1), _lib.DC_INVALID_ARGUMENT, r"takes \(B, H, L, E\) tensors"),
     (dict(dtype=7), _lib.DC_INVALID_ARGUMENT, "dtype"),
+    (dict(flags=2), _lib.DC_INVALID_ARGUMENT, "flags has unknown bits"),
     (dict(q_len=2**31), _lib.DC_UNSUPPORTED, "2\\^31"),
 ])
 def test_forward_argument_errors(kw, status, msg):
@@ -176,15 +178,16 @@ def test_decode_workspace_covers_splits():
 def test_schedule_layout_matches_header(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "dc_attn.h"\n'
-                   "int main(void){printf(\"%zu %zu %zu\\n\", sizeof(dc_sdpa_schedule),"
-                   " offsetof(dc_sdpa_schedule, deterministic), offsetof(dc_sdpa_schedule, workgroups));"
+                   "int main(void){printf(\"%zu %zu %zu %zu\\n\", sizeof(dc_sdpa_schedule),"
+                   " offsetof(dc_sdpa_schedule, deterministic), offsetof(dc_sdpa_schedule, workgroups),"
+                   " offsetof(dc_sdpa_schedule, chunks));"
                    "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
     got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True,
                                        check=True).stdout.split()))
     S = _lib.Schedule
-    assert got == [ctypes.sizeof(S), S.deterministic.offset, S.workgroups.offset]
+    assert got == [ctypes.sizeof(S), S.deterministic.offset, S.workgroups.offset, S.chunks.offset]
 
 
 def test_schedule_query_is_a_dry_run():

@@ -263,8 +263,18 @@ def test_causal_with_mask(oracle_lib):
     _check(oracle_lib, q, k, v, g, True, 0.2, mask, tag="causal+mask")
 
 
-@pytest.mark.parametrize("E,factor", [(64, 2), (128, 8)])
-def test_large_logits(oracle_lib, E, factor):
+@pytest.fixture
+def consistent_scores(request):
+    """Run the test with DC_FLAG_CONSISTENT_SCORES on (param True) or off, restoring the setting."""
+    from densecore_amd import _native
+    previous = _native.consistent_scores(getattr(request, "param", False))
+    yield getattr(request, "param", False)
+    _native.consistent_scores(previous)
+
+
+@pytest.mark.parametrize("E,factor,consistent_scores", [(64, 2, False), (128, 8, False), (128, 2, True)],
+                         indirect=["consistent_scores"])
+def test_large_logits(oracle_lib, E, factor, consistent_scores):
     """Scores far past the exp_u20 bound (|x - max| > 87.3, the reference's SLEEF fallback).
 
     Forward at the standard tolerance.  The gradients of such a peaked softmax are
@@ -276,8 +286,10 @@ def test_large_logits(oracle_lib, E, factor):
     sums to one by ~1e-5, an error of the test, not of either implementation.)  At head dim 128
     the backward's scores run on 16x16x4 products in another order than the forward's 32x32x2
     (its 8-wave layout), which is that same mixing inside the GPU: its error there is held to
-    8x the oracle's (measured up to 5.3x, in dV).  q and k scale with E^(-1/4), so the score
-    gaps within a row stay of the order of 100 at both head dims."""
+    8x the oracle's (measured up to 5.3x, in dV).  With DC_FLAG_CONSISTENT_SCORES the head-dim-128
+    backward forms its scores in the forward's order and is held to 2x, as at head dim 64.  q and
+    k scale with E^(-1/4), so the score gaps within a row stay of the order of 100 at both head
+    dims."""
     from oracle import brute
     rng = np.random.default_rng(9)
     q, k, v, g = (rng.standard_normal((1, 2, 96, E), dtype=np.float32) for _ in range(4))
@@ -384,3 +396,30 @@ def test_unaligned_pointers(oracle_lib, E):
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv"), got, ref):
         assert_f32(a.cpu().numpy(), b, f"unaligned {name}")
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,causal,masked", [
+    (1, 8, 8, 2048, 2048, True, False),    # stream-K ranges
+    (8, 12, 12, 512, 512, True, False),    # whole tiles
+    (2, 4, 2, 300, 700, True, False),      # grouped heads, keys past the queries
+    (1, 2, 2, 700, 300, False, True),      # float mask, L > S
+    (2, 3, 3, 190, 190, True, True),       # causal and a mask
+])
+def test_consistent_scores_backward(oracle_lib, B, H, Hkv, L, S, causal, masked):
+    """DC_FLAG_CONSISTENT_SCORES at head dim 128 (the forward-ordered 4-wave backward tile): the
+    float32 bar against the oracle, on the whole-tile and stream-K schedules, with grouped heads,
+    L != S and masks; and the same results as the default tile to the bar."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(B * 100 + H + L + S)
+    q, g = (rng.standard_normal((B, H, L, 128), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, Hkv, S, 128), dtype=np.float32) for _ in range(2))
+    mask = None
+    if masked:
+        mask = rng.standard_normal((B, H, L, S)).astype(np.float32)
+        mask[rng.random((B, H, L, S)) < 0.2] = -np.inf
+    print(f"[case] consistent scores B{B} H{H} Hkv{Hkv} L{L} S{S} causal={causal} mask={masked}", flush=True)
+    previous = _native.consistent_scores(True)
+    try:
+        _check(oracle_lib, q, k, v, g, causal, None, mask, tag="consistent")
+    finally:
+        _native.consistent_scores(previous)
