@@ -143,9 +143,11 @@ size_t fwd_partial_ws(const dc::AttnShape &s) {
 }
 size_t fwd_exp_ws(const dc::AttnShape &s) { return round_up((size_t)s.B * s.Hkv * sizeof(int)); }
 size_t fwd_ws(const dc::AttnShape &s, bool bf16) {
-    if (s.E > dc::kFlashMaxHeadDim) return dc::wide_ws_bytes(s, bf16, false);  // required, not optional
+    if (s.E > dc::flash_max_head_dim(bf16)) return dc::wide_ws_bytes(s, bf16, false);  // required, not optional
     size_t n = fwd_order_ws(s);
-    if (bf16) n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s) + round_up(dc::fwd_bf16_split_bytes(s));
+    // bf16 up to head dim 128: the fp16 copy of V for the P V product (above, P enters as bf16 hi + lo).
+    if (bf16 && s.E <= dc::kFlashMaxHeadDim)
+        n += fwd_v16_ws(s) + fwd_partial_ws(s) + fwd_exp_ws(s) + round_up(dc::fwd_bf16_split_bytes(s));
     else n += round_up(dc::fwd_f32_split_bytes(s));
     return n;
 }
@@ -168,7 +170,7 @@ BwdLayout bwd_layout(const dc::AttnShape &s, bool bf16) {
     };
     l.dsum = take((size_t)s.B * s.H * s.L * sizeof(float));
     l.part = at;
-    if (s.E > dc::kFlashMaxHeadDim) {  // head dims above 128: the materialized path's buffers
+    if (s.E > dc::flash_max_head_dim(bf16)) {  // beyond the flash kernels: the materialized path's buffers
         take(dc::wide_ws_bytes(s, bf16, true));
         l.total = at;
         return l;
@@ -370,11 +372,12 @@ dc_status dc_sdpa_fwd(const dc_attn_desc *d, const void *q, const void *k, const
         return fail(DC_INVALID_ARGUMENT, kNullMsg);
     s.vec = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     dc::FwdArgs a{s, q, k, v, out, lse, nullptr, nullptr, nullptr, nullptr, nullptr};
-    if (s.E > dc::kFlashMaxHeadDim) {  // materialized over row blocks in the workspace (wide.hip)
+    if (s.E > dc::flash_max_head_dim(d->dtype == DC_BF16)) {  // materialized over row blocks (wide.hip)
         const bool bf16 = d->dtype == DC_BF16;
         if (workspace == nullptr || dc::wide_rows(s, bf16, false, workspace_bytes) <= 0)
             return fail(DC_INVALID_ARGUMENT,
-                        "flash attention forward with head_dim above 128 needs a workspace of "
+                        "flash attention forward with head_dim above the flash kernels' (128 for float32, "
+                        "256 for bfloat16) needs a workspace of "
                         "dc_sdpa_fwd_workspace_size bytes (at least one row of scores per kv head)");
         hipStream_t strm = static_cast<hipStream_t>(stream);
         dc_status st2 = launched(dc::launch_wide_fwd(a, bf16, workspace, workspace_bytes, strm));
@@ -465,10 +468,11 @@ dc_status dc_sdpa_bwd(const dc_attn_desc *d, const void *grad_out, const void *q
         if (st != DC_OK) return st;
         return launched(dc::launch_bwd_ref_nan(a, bf16, strm));
     }
-    if (s.E > dc::kFlashMaxHeadDim) {  // materialized over row blocks after dsum (wide.hip)
+    if (s.E > dc::flash_max_head_dim(bf16)) {  // materialized over row blocks after dsum (wide.hip)
         if (dc::wide_rows(s, bf16, true, workspace_bytes - l.part) <= 0)
             return fail(DC_INVALID_ARGUMENT,
-                        "flash attention backward with head_dim above 128 needs a workspace of "
+                        "flash attention backward with head_dim above the flash kernels' (128 for float32, "
+                        "256 for bfloat16) needs a workspace of "
                         "dc_sdpa_bwd_workspace_size bytes (at least one row of scores per kv head)");
         st = launched(dc::launch_wide_bwd(a, bf16, ws + l.part, workspace_bytes - l.part, strm));
     } else {

@@ -48,26 +48,39 @@ namespace {
 // ---------------------------------------------------------------------------------------
 // dK / dV (keys stationary)
 // ---------------------------------------------------------------------------------------
-constexpr int kKW = 8;             // waves
+constexpr int kKW = 8;             // waves (head dims up to 128)
 constexpr int kKThreads = 64 * kKW;
-constexpr int kKN = 128;           // keys per workgroup
+constexpr int kKN = 128;           // keys per workgroup (head dims up to 128; split grids)
 constexpr int kKM = 64;            // queries per step
+
+// The dK/dV workgroup: up to head dim 128, 8 waves over 128 keys with each step's Q and dO tiles
+// double-buffered; at 256, where a 64-row tile takes 34 KB, 4 waves over 64 keys with one Q / dO
+// buffer: 136 KB of LDS, one workgroup per CU and one wave per SIMD, whose 512 registers hold the
+// 2 x 256-dim dK / dV accumulators of its 32 keys.
+template <int D>
+struct KLayout {
+    static constexpr int W = D > 128 ? 4 : kKW;          // waves
+    static constexpr int N = 16 * W;                     // keys (32 per pair of waves)
+    static constexpr int QB = D > 128 ? 1 : 2;           // Q / dO buffers
+    static constexpr int THREADS = 64 * W;
+};
 
 template <int D>
 struct alignas(16) DkdvSmem {
-    using TK = CMTile<kKN, D>;
+    using TK = CMTile<KLayout<D>::N, D>;
     using TQ = CMTile<kKM, D>;
+    static constexpr int QB = KLayout<D>::QB;
     struct Main {
         u32x4 k[TK::SLOTS];
         u32x4 v[TK::SLOTS];
-        u32x4 q[2][TQ::SLOTS];
-        u32x4 o[2][TQ::SLOTS];
-        float lse[2][kKM];
-        float dsum[2][kKM];
+        u32x4 q[QB][TQ::SLOTS];
+        u32x4 o[QB][TQ::SLOTS];
+        float lse[QB][kKM];
+        float dsum[QB][kKM];
     };
     // End of the sweep: the second wave of each pair hands its partial dK^T, dV^T over.
     struct Red {
-        float acc[4][2 * (D / 32)][16][64];
+        float acc[KLayout<D>::W / 2][2 * (D / 32)][16][64];
     };
     union {
         Main m;
@@ -137,15 +150,17 @@ __host__ __device__ inline int dkdv_pieces(const AttnShape &s, int kt, int chunk
 }
 
 template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16, bool SPLIT = false>
-__global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
+__global__ __launch_bounds__(KLayout<D>::THREADS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32;
+    constexpr int KW = KLayout<D>::W, KN = KLayout<D>::N, QB = KLayout<D>::QB;
+    static_assert(!SPLIT || KN == kKN, "split grids are planned over 128-key tiles");
     __shared__ DkdvSmem<D> sm;
 
     const AttnShape &s = a.s;
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kw = wave & 3, qh = wave >> 2;
-    const int nkt = (s.S + kKN - 1) / kKN;
+    const int kw = wave % (KW / 2), qh = wave / (KW / 2);
+    const int nkt = (s.S + KN - 1) / KN;
     const int w = logical_block();
     int bhk = w / nkt, kt_ = w % nkt;  // causal: small n0 (most queries) first
     // Split: blocks run over (kv head, key tile, piece), the pieces of a key tile adjacent.
@@ -163,7 +178,7 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         if (bhk >= s.B * s.Hkv || kt_ >= nkt) return;  // not reached: the grid holds the pieces
         piece = r, npieces = dkdv_pieces(s, kt_, a.chunk_k);
     }
-    const int n0 = kt_ * kKN;
+    const int n0 = kt_ * KN;
     const int b = bhk / s.Hkv, hk = bhk % s.Hkv;
     const int kw0 = n0 + 32 * kw;
     const int key = kw0 + lr;  // this lane's key column
@@ -173,9 +188,9 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     F16Scales fs;
     if constexpr (F16) fs = f16_scales(a, bhk);
     const float sc_log2 = F16 ? fs.sc_log2 : s.scale_log2, sc = F16 ? fs.sc : s.scale;
-    const int nkeys = min(kKN, s.S - n0);
-    fill_cm<kKN, D, VEC, kKW>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
-    fill_cm<kKN, D, VEC, kKW>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
+    const int nkeys = min(KN, s.S - n0);
+    fill_cm<KN, D, VEC, KW>(sm.m.k, kb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
+    fill_cm<KN, D, VEC, KW>(sm.m.v, vb + (int64_t)n0 * s.E, nkeys, s.E, wave, lane);
 
     const int m_begin = CAUSAL ? n0 : 0;  // n0 is a multiple of kKM
     const int per_head = s.L > m_begin ? (s.L - m_begin + kKM - 1) / kKM : 0;
@@ -186,11 +201,11 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     auto step_bh = [&](int i) { return b * s.H + hk * s.repeat + i / per_head; };
     auto step_m0 = [&](int i) { return m_begin + (i % per_head) * kKM; };
     auto fill_step = [&](int i) {
-        const int bh = step_bh(i), m0 = step_m0(i), buf = i & 1;
+        const int bh = step_bh(i), m0 = step_m0(i), buf = i % QB;
         const int rows = min(kKM, s.L - m0);
         const int64_t off = ((int64_t)bh * s.L + m0) * s.E;
-        fill_cm<kKM, D, VEC, kKW>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, lane);
-        fill_cm<kKM, D, VEC, kKW>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, lane);
+        fill_cm<kKM, D, VEC, KW>(sm.m.q[buf], static_cast<const __bf16 *>(a.q) + off, rows, s.E, wave, lane);
+        fill_cm<kKM, D, VEC, KW>(sm.m.o[buf], static_cast<const __bf16 *>(a.dout) + off, rows, s.E, wave, lane);
     };
     // -lse log2 e (-inf past L: P = 0 there) and -dsum of a step, one value per lane of waves
     // 0 and 1.  (The float32 kernels subtract lse in natural-log units first, which saves one
@@ -204,16 +219,16 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         return F16 ? ldexpf(ds, fs.e_pv) : ds;
     };
     auto store_row_stat = [&](int i, float x) {
-        if (wave == 0) sm.m.lse[i & 1][lane] = x;
-        else sm.m.dsum[i & 1][lane] = x;
+        if (wave == 0) sm.m.lse[i % QB][lane] = x;
+        else sm.m.dsum[i % QB][lane] = x;
     };
-    if (i_begin < nsteps) {
+    if (QB == 2 && i_begin < nsteps) {
         fill_step(i_begin);
         if (wave < 2) store_row_stat(i_begin, load_row_stat(i_begin));
     }
 
     const uint32_t rowb = row_lanebase<kKM, D>(lane);
-    const uint32_t rowbk = row_lanebase<kKN, D>(lane);
+    const uint32_t rowbk = row_lanebase<KN, D>(lane);
     const uint32_t trb = tr_lanebase<kKM, D>(lane);
 
     f32x16 dk[NDT], dv[NDT];
@@ -223,13 +238,22 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
         for (int r = 0; r < 16; ++r) dk[dt][r] = 0.f, dv[dt][r] = 0.f;
 
     for (int i = i_begin; i < nsteps; ++i) {
-        const int bh = step_bh(i), h = bh - b * s.H, m0 = step_m0(i), buf = i & 1;
-        if (VEC) wait_vmem();
-        __syncthreads();  // step i's tiles landed (and K/V at i = 0); step i - 1 is done
+        const int bh = step_bh(i), h = bh - b * s.H, m0 = step_m0(i), buf = i % QB;
         float stat = 0.f;
-        if (i + 1 < nsteps) {
-            if (wave < 2) stat = load_row_stat(i + 1);
-            fill_step(i + 1);
+        if constexpr (QB == 2) {
+            if (VEC) wait_vmem();
+            __syncthreads();  // step i's tiles landed (and K/V at i = 0); step i - 1 is done
+            if (i + 1 < nsteps) {
+                if (wave < 2) stat = load_row_stat(i + 1);
+                fill_step(i + 1);
+            }
+        } else {
+            // One buffer: step i's tiles are loaded once step i - 1 is done with the buffer.
+            if (i > i_begin) __syncthreads();
+            fill_step(i);
+            if (wave < 2) store_row_stat(i, load_row_stat(i));
+            if (VEC) wait_vmem();
+            __syncthreads();  // step i's tiles landed (and K/V at the first step)
         }
 
         const int mq = m0 + 32 * qh;  // this wave's 32 queries
@@ -254,9 +278,9 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 #pragma unroll
             for (int st = 0; st < KSTEP; ++st) {
                 sacc = mfma16<F16>(row_frag<kKM, D>(qt, rowb, 32 * qh, st),
-                                   row_frag<kKN, D>(sm.m.k, rowbk, 32 * kw, st), sacc);
+                                   row_frag<KN, D>(sm.m.k, rowbk, 32 * kw, st), sacc);
                 pacc = mfma16<F16>(row_frag<kKM, D>(ot, rowb, 32 * qh, st),
-                                   row_frag<kKN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
+                                   row_frag<KN, D>(sm.m.v, rowbk, 32 * kw, st), pacc);
             }
             // Keep the operand reads (two per MFMA) four MFMAs ahead of their use.
             sched_reads_ahead<2 * KSTEP, 2, 4>();
@@ -335,7 +359,7 @@ __global__ __launch_bounds__(kKThreads) void bwd_dkdv_bf16_kernel(BwdArgs a) {
                 }
             }
         }
-        if (i + 1 < nsteps && wave < 2) store_row_stat(i + 1, stat);
+        if (QB == 2 && i + 1 < nsteps && wave < 2) store_row_stat(i + 1, stat);
     }
 
     // Sum the two partials of each key group (waves kw and kw + 4) and write dK, dV.  The
@@ -428,8 +452,12 @@ struct alignas(16) DqSmem {
     u32x4 v[2][T::SLOTS];
 };
 
+// Waves per SIMD of the dQ kernel: two workgroups per CU up to head dim 128; at 256 its K/V tiles
+// take 136 KB of LDS and its Q, dO and dQ registers 256 per lane: one workgroup, one wave per SIMD.
+constexpr int dq_waves_per_eu(int D) { return D > 128 ? 1 : 2; }
+
 template <int D, bool CAUSAL, bool MASK, bool VEC, bool F16, bool SPLIT = false>
-__global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(dq_waves_per_eu(D), dq_waves_per_eu(D)))) void bwd_dq_bf16_kernel(BwdArgs a) {
     constexpr int KSTEP = D / 16, NDT = D / 32, NT = kQN / 32;
     __shared__ DqSmem<D> sm;
 
@@ -708,6 +736,7 @@ struct BwdSplitPlan {
 
 template <int D>
 BwdSplitPlan plan_bwd(const AttnShape &s) {
+    static_assert(D <= 128, "head dims above 128 run whole grids");
     BwdSplitPlan p;
     if (s.mask != nullptr || s.L == 0 || s.S == 0) return p;
     const int nkt = (s.S + kKN - 1) / kKN;
@@ -778,7 +807,8 @@ hipError_t launch_split(const BwdArgs &args, const BwdSplitPlan &p, hipStream_t 
 template <int D, bool VEC, bool F16>
 hipError_t launch_dvf(const BwdArgs &a, hipStream_t st) {
     const bool mask = a.s.mask != nullptr, causal = a.s.causal;
-    const dim3 gk(((a.s.S + kKN - 1) / kKN) * a.s.B * a.s.Hkv), bk(kKThreads);
+    constexpr int KN = KLayout<D>::N;
+    const dim3 gk(((a.s.S + KN - 1) / KN) * a.s.B * a.s.Hkv), bk(KLayout<D>::THREADS);
     const dim3 gq(((a.s.L + kQM - 1) / kQM) * a.s.B * a.s.H), bq(kQThreads);
     if (a.s.S > 0) {
         if (causal && mask) return_if(launch(bwd_dkdv_bf16_kernel<D, true, true, VEC, F16>, gk, bk, st, a));
@@ -810,12 +840,14 @@ hipError_t launch_dv(const BwdArgs &a, hipStream_t st) {
     return_if(launch_to_f16(copies, 4, n, a.f16_partial, st));
     BwdArgs f = a;
     f.q = a.q16, f.k = a.k16, f.v = a.v16, f.dout = a.do16;
-    if (a.split) {
-        const BwdSplitPlan p = plan_bwd<D>(a.s);
-        if ((p.chunk_k > 0 || p.chunk_q > 0) && p.bytes <= a.split_bytes) {
-            record_schedule(split_chunk_k, p.chunk_k);
-            record_schedule(split_chunk_q, p.chunk_q);
-            return launch_split<D, VEC>(f, p, st);
+    if constexpr (D <= 128) {
+        if (a.split) {
+            const BwdSplitPlan p = plan_bwd<D>(a.s);
+            if ((p.chunk_k > 0 || p.chunk_q > 0) && p.bytes <= a.split_bytes) {
+                record_schedule(split_chunk_k, p.chunk_k);
+                record_schedule(split_chunk_q, p.chunk_q);
+                return launch_split<D, VEC>(f, p, st);
+            }
         }
     }
     return launch_dvf<D, VEC, true>(f, st);
@@ -834,7 +866,8 @@ size_t bwd_bf16_split_bytes(const AttnShape &s) {
     if (s.B * s.Hkv == 0 || s.L == 0 || s.S == 0) return 0;
     if (s.E <= 32) return plan_bwd<32>(s).bytes;
     if (s.E <= 64) return plan_bwd<64>(s).bytes;
-    return plan_bwd<128>(s).bytes;
+    if (s.E <= 128) return plan_bwd<128>(s).bytes;
+    return 0;  // head dims above 128: no split
 }
 
 hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st) {
@@ -845,7 +878,8 @@ hipError_t launch_bwd_bf16(const BwdArgs &a, hipStream_t st) {
     if (a.s.B * a.s.Hkv == 0) return hipSuccess;
     if (a.s.E <= 32) return launch_d<32>(a, st);
     if (a.s.E <= 64) return launch_d<64>(a, st);
-    return launch_d<128>(a, st);
+    if (a.s.E <= 128) return launch_d<128>(a, st);
+    return launch_d<256>(a, st);
 }
 
 }  // namespace dc

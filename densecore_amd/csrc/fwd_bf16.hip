@@ -51,8 +51,13 @@ DEVI void fill_tile(KVTileBf16<D> &t, const __bf16 *kb, const __bf16 *vb, int n0
     fill_cm<kBN, D, VEC, kWaves>(t.v, vb + (int64_t)n0 * E, S - n0, E, wave, lane);
 }
 
+// Waves per SIMD of the 4-wave kernel: two workgroups per CU up to head dim 128; at 256 its K/V
+// tiles take 136 KB of LDS and its queries and output 192 registers per lane, so one workgroup
+// per CU and one wave per SIMD (512 registers).
+constexpr int fwd_waves_per_eu(int D) { return D > 128 ? 1 : 2; }
+
 template <int D, bool CAUSAL, bool MASK, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(fwd_waves_per_eu(D), fwd_waves_per_eu(D)))) void fwd_bf16_kernel(FwdArgs a) {
     constexpr int NT = kBN / 32;  // 32-key sub-tiles per tile
     constexpr int KSTEP = D / 16; // MFMA k-steps over the head dim
     constexpr int NDT = D / 32;   // 32-dim output tiles
@@ -577,6 +582,16 @@ FwdSplitPlan plan(const AttnShape &s) {
 template <int D, bool VEC>
 hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
     const bool mask = a.s.mask != nullptr;
+    if constexpr (D > 128) {
+        // Head dims 129-256: the 4-wave kernel, with or without a mask (the ping-pong kernel's
+        // 8 waves would need more than 256 registers each); P enters P V as bf16 hi + lo.
+        const int nqt = (a.s.L + kBM - 1) / kBM;
+        const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
+        if (a.s.causal && mask) return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
+        if (a.s.causal) return launch(fwd_bf16_kernel<D, true, false, VEC>, grid, block, st, a);
+        if (mask) return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
+        return launch(fwd_bf16_kernel<D, false, false, VEC>, grid, block, st, a);
+    }
     if (!mask) {
         const int nqt = (a.s.L + kPPM - 1) / kPPM;
         const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
@@ -628,14 +643,16 @@ size_t fwd_bf16_split_bytes(const AttnShape &s) {
     if (s.B == 0 || s.H == 0 || s.L == 0) return 0;
     if (s.E <= 32) return plan<32>(s).bytes;
     if (s.E <= 64) return plan<64>(s).bytes;
-    return plan<128>(s).bytes;
+    if (s.E <= 128) return plan<128>(s).bytes;
+    return 0;  // head dims above 128: no split
 }
 
 hipError_t launch_fwd_bf16(const FwdArgs &a, hipStream_t st) {
     if (a.s.B == 0 || a.s.H == 0 || a.s.L == 0) return hipSuccess;
     if (a.s.E <= 32) return launch_d<32>(a, st);
     if (a.s.E <= 64) return launch_d<64>(a, st);
-    return launch_d<128>(a, st);
+    if (a.s.E <= 128) return launch_d<128>(a, st);
+    return launch_d<256>(a, st);
 }
 
 }  // namespace dc

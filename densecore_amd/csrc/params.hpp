@@ -126,7 +126,9 @@ size_t wide_ws_bytes(const AttnShape &s, bool bf16, bool backward);
 int64_t wide_rows(const AttnShape &s, bool bf16, bool backward, size_t bytes);
 hipError_t launch_wide_fwd(const FwdArgs &a, bool bf16, void *ws, size_t bytes, hipStream_t st);
 hipError_t launch_wide_bwd(const BwdArgs &a, bool bf16, void *ws, size_t bytes, hipStream_t st);
-constexpr int kFlashMaxHeadDim = 128;  // the flash kernels' widest instantiation
+constexpr int kFlashMaxHeadDim = 128;      // the float32 flash kernels' widest instantiation
+constexpr int kFlashMaxHeadDimBf16 = 256;  // the bf16 flash kernels' widest instantiation
+inline int flash_max_head_dim(bool bf16) { return bf16 ? kFlashMaxHeadDimBf16 : kFlashMaxHeadDim; }
 
 // Rows the reference's blocking fixes (ref_rows.hip): causal attention with a scale that is not
 // positive, or a NaN scale.  The forward pass overwrites the rows the reference makes NaN (or 0);

@@ -242,7 +242,7 @@ def test_bmm_descriptor_layout_matches_header(tmp_path):
 
 
 def test_wide_head_dims_take_the_materialized_path():
-    """Head dims above 128 run materialized over row blocks in the workspace (any head dim, as
+    """Head dims above the flash kernels' (128 float32, 256 bf16) run materialized over row blocks in the workspace (any head dim, as
     the reference's kernels take any): the schedule query reports the rows per block, the
     workspace is required, and a smaller one only shortens the blocks."""
     L = _lib.lib()
@@ -253,10 +253,28 @@ def test_wide_head_dims_take_the_materialized_path():
         assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, full, ctypes.byref(out)) == _lib.DC_OK
         assert out.materialized_rows == 2 * 50  # repeat (4 / 2) x L rows per (batch, kv head)
         assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, 0, ctypes.byref(out)) == _lib.DC_INVALID_ARGUMENT
-        assert b"head_dim above 128 needs a workspace" in L.dc_last_error()
+        assert b"head_dim above the flash kernels' (128 for float32, 256 for bfloat16)" in L.dc_last_error()
         one_row = full - (2 * 50 - 1) * 2 * 2 * 70 * 4  # full minus 99 rows of (items x S) floats
         assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, one_row, ctypes.byref(out)) == _lib.DC_OK
         assert 1 <= out.materialized_rows < 2 * 50
         bw = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
         assert L.dc_sdpa_bwd_schedule(ctypes.byref(d), 0, bw, ctypes.byref(out)) == _lib.DC_OK
         assert out.materialized_rows == 2 * 50 and out.deterministic == 1
+
+
+def test_bf16_head_dims_to_256_take_the_flash_kernels():
+    """bf16 head dims 129-256 run on the flash kernels (no materialized rows, no workspace needed);
+    float32 ones run materialized."""
+    L = _lib.lib()
+    out = _lib.Schedule()
+    for E in (129, 200, 256):
+        d = desc(head_dim=E, dtype=_lib.DC_BF16, q_len=50, kv_len=70)
+        assert L.dc_sdpa_fwd_schedule(ctypes.byref(d), 0, 0, ctypes.byref(out)) == _lib.DC_OK
+        assert out.materialized_rows == 0
+        bw = L.dc_sdpa_bwd_workspace_size(ctypes.byref(d))
+        assert L.dc_sdpa_bwd_schedule(ctypes.byref(d), 0, bw, ctypes.byref(out)) == _lib.DC_OK
+        assert out.materialized_rows == 0 and out.f16_products == 1 and out.deterministic == 1
+        d32 = desc(head_dim=E, dtype=_lib.DC_F32, q_len=50, kv_len=70)
+        full = L.dc_sdpa_fwd_workspace_size(ctypes.byref(d32))
+        assert L.dc_sdpa_fwd_schedule(ctypes.byref(d32), 0, full, ctypes.byref(out)) == _lib.DC_OK
+        assert out.materialized_rows > 0

@@ -325,3 +325,49 @@ def test_bf16_long_causal_early_keys():
         bar = 2.0 ** -7 * np.abs(r) + 3e-4 * np.sqrt(np.mean(r ** 2))
         err = np.abs(got[name] - r)
         assert np.all(err <= bar), f"{name}: max err / bar {np.max(err / bar):.3f}"
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,E,causal,mask", [
+    (2, 4, 2, 300, 300, 256, True, None),
+    (1, 2, 2, 2048, 2048, 256, True, None),     # long causal rows (fp16 P with its low part)
+    (2, 3, 3, 130, 257, 192, False, None),
+    (1, 2, 1, 200, 120, 256, True, None),       # L > S, grouped heads
+    (2, 2, 2, 97, 150, 256, False, "float"),   # a float mask with -inf holes, a fully masked row
+    (3, 2, 2, 64, 200, 200, False, "padding"),  # key padding, head dim not a multiple of 32
+    (2, 2, 2, 40, 5, 129, False, None),
+])
+def test_bf16_flash_head_dims_to_256(oracle_lib, B, H, Hkv, L, S, E, causal, mask):
+    """bf16 head dims 129-256 on the flash kernels (4-wave forward, dQ and dK/dV kernels at head
+    dim 256, one wave per SIMD): no materialized rows; out and lse against the oracle on the upcast
+    inputs, the backward from the GPU's own (out, lse), bf16 bar; the backward bit-identical from
+    run to run."""
+    from densecore_amd import _native
+    rng = np.random.default_rng(L * 3 + S + E + B)
+    q, g = (bf16_round(rng.standard_normal((B, H, L, E), dtype=np.float32)) for _ in range(2))
+    k, v = (bf16_round(rng.standard_normal((B, Hkv, S, E), dtype=np.float32)) for _ in range(2))
+    mk = tm = None
+    if mask == "float":
+        mk = rng.standard_normal((B, H, L, S)).astype(np.float32)
+        mk[rng.random((B, H, L, S)) < 0.25] = -np.inf
+        mk[0, 0, 1] = -np.inf
+        tm = torch.from_numpy(mk).to(DEV)
+    elif mask == "padding":
+        lengths = rng.integers(1, S + 1, size=B)
+        m1 = np.where(np.arange(S)[None, :] < lengths[:, None], np.float32(0), np.float32(-np.inf))
+        tm = torch.from_numpy(m1[:, None, None, :]).to(DEV).expand(B, H, L, S)
+        mk = np.ascontiguousarray(np.broadcast_to(m1[:, None, None, :], (B, H, L, S)))
+    print(f"[case] bf16 flash B{B} H{H} Hkv{Hkv} L{L} S{S} E{E} causal={causal} mask={mask}", flush=True)
+    tq, tk, tv, tg = (_bf(x) for x in (q, k, v, g))
+    fs = _native._schedule(False, tq, tk, tv, causal, mask=tm)
+    bs = _native._schedule(True, tq, tk, tv, causal, mask=tm)
+    assert fs["materialized_rows"] == 0 and bs["materialized_rows"] == 0 and bs["deterministic"] == 1, (fs, bs)
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, None, mk)
+    out, lse = _native._flash_attention(tq, tk, tv, causal, None, tm)
+    assert_bf16(_np(out), ref_o, "out")
+    assert_bf16(_np(lse), ref_l, "lse")
+    ref = oracle_lib.backward(g, q, k, v, _np(out), _np(lse), causal, None, mk)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, causal, None, tm)
+    again = _native._flash_attention_backward(tg, tq, tk, tv, out, lse, causal, None, tm)
+    for name, a, b, c in zip(("dq", "dk", "dv"), got, ref, again):
+        assert_bf16(_np(a), b, name)
+        assert torch.equal(a, c), f"{name}: runs differ"

@@ -76,7 +76,9 @@ FWD = [  # tag, B, H, Hkv, L, S, E, causal, bf16, mask, expected plan
     ("bf16_split", 1, 2, 2, 2048, 2048, 128, True, True, None, "split"),
     ("bf16_grouped", 2, 16, 8, 1024, 1024, 128, True, True, None, "any"),
     ("f32_wide_rows", 1, 2, 2, 200, 300, 160, True, False, None, "rows"),
-    ("bf16_wide_rows", 2, 2, 1, 150, 150, 256, False, True, None, "rows"),
+    ("bf16_wide_rows", 2, 2, 1, 150, 150, 320, False, True, None, "rows"),
+    ("bf16_flash_d256", 2, 4, 2, 300, 300, 256, True, True, None, "whole"),
+    ("bf16_flash_d200_padding", 3, 2, 2, 100, 250, 200, False, True, "padding", "any"),
 ]
 
 
@@ -132,6 +134,8 @@ BWD = [  # tag, B, H, Hkv, L, S, E, causal, bf16, workspace bytes ("full", "min"
     ("bf16_masked_whole", 2, 8, 4, 600, 700, 128, False, True, "full", "whole"),
     ("bf16_split", 1, 2, 2, 2048, 2048, 128, True, True, "full", "split"),
     ("f32_wide_rows", 1, 2, 2, 200, 300, 192, True, False, "rows", "rows"),
+    ("bf16_flash_d256", 2, 4, 2, 300, 300, 256, True, True, "full", "whole"),
+    ("bf16_flash_d256_min", 1, 2, 2, 200, 260, 256, False, True, "min", "any"),
 ]
 
 
@@ -160,7 +164,9 @@ def test_backward_writes_in_bounds(oracle_lib, tag, B, H, Hkv, L, S, E, causal, 
         nbytes = _ws_for_rows(True, tq, tk, tv, causal, full, (H // Hkv) * L // 3)
     sched = _native._schedule(True, tq, tk, tv, causal, mask=tm, workspace_bytes=nbytes)
     print(f"[schedule] {sched}", flush=True)
-    expect = {"whole": lambda s: s["streamk_ranges"] == 0 and s["split_chunk_k"] == 0 and s["chunks"] == 1,
+    expect = {"whole": lambda s: s["streamk_ranges"] == 0 and s["split_chunk_k"] == 0 and s["chunks"] == 1
+                       and s["materialized_rows"] == 0,
+              "any": lambda s: True,
               "streamk": lambda s: s["streamk_ranges"] > 0 and s["deterministic"] == 1,
               "atomics": lambda s: s["deterministic"] == 0,
               "pieces": lambda s: s["chunks"] > 1 and s["deterministic"] == 1,
