@@ -254,6 +254,16 @@ __host__ __device__ inline int64_t chunk_of(const StreamK &k, int64_t p) {
     return ((p + 1) * k.chunks - 1) / k.total;
 }
 
+// The thread index through an empty asm, which the compiler cannot see through.  A key tile's
+// prologue (K / V loads) and epilogue (dK / dV stores) derive their lane addresses from such a
+// copy: in the stream-K kernel, which runs key tiles in a loop, the compiler would otherwise hoist
+// that address arithmetic out of the loop and hold it in registers across every step of every
+// tile, and spill (the step loop's own addresses use the thread index directly).
+DEVI int opaque_index(int tid) {
+    asm volatile("" : "+v"(tid));
+    return tid;
+}
+
 // Steps [i0, i1) of key tile kt of (batch, kv head) bhk, by one workgroup.  The workgroup's dK
 // (times scale) and dV for the tile's keys go to kdst / vdst (the tile's first key row, row
 // stride E): the outputs when these are all of the tile's steps, or the partial slot of the
@@ -281,16 +291,18 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     // would not fit one wave's registers without spills.
     constexpr bool KREG = D <= 64;
     float kreg[KREG ? DH : 1], vreg[DH];
+    const int ptid = opaque_index(tid);  // the prologue's own copy (see opaque_index)
+    const int pkey = kw0 + (ptid & 31), pg = (ptid & 63) >> 5;
     {
-        const float *kr = kb + (int64_t)key * s.E, *vr = vb + (int64_t)key * s.E;
-        if (VEC && key < s.S) {
+        const float *kr = kb + (int64_t)pkey * s.E, *vr = vb + (int64_t)pkey * s.E;
+        if (VEC && pkey < s.S) {
 #pragma unroll
             for (int t = 0; t < DH; t += 4) {
-                const f32x4 y = *reinterpret_cast<const f32x4 *>(vr + g * DH + t);
+                const f32x4 y = *reinterpret_cast<const f32x4 *>(vr + pg * DH + t);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) vreg[t + u] = y[u];
                 if constexpr (KREG) {
-                    const f32x4 x = *reinterpret_cast<const f32x4 *>(kr + g * DH + t);
+                    const f32x4 x = *reinterpret_cast<const f32x4 *>(kr + pg * DH + t);
 #pragma unroll
                     for (int u = 0; u < 4; ++u) kreg[t + u] = x[u];
                 }
@@ -298,8 +310,8 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         } else {
 #pragma unroll
             for (int t = 0; t < DH; ++t) {
-                const int d = g * DH + t;
-                const bool ok = key < s.S && d < s.E;
+                const int d = pg * DH + t;
+                const bool ok = pkey < s.S && d < s.E;
                 if constexpr (KREG) kreg[t] = ok ? kr[d] : 0.f;
                 vreg[t] = ok ? vr[d] : 0.f;
             }
@@ -308,7 +320,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     // The workgroup's K tile, transposed into LDS for the dQ product (lanes along keys, so
     // the LDS writes are conflict-free).
     if (VEC) {
-        for (int i = tid; i < kBN * (D / 4); i += kThreads) {
+        for (int i = ptid; i < kBN * (D / 4); i += kThreads) {
             const int r = i % kBN, c = (i / kBN) * 4, kk = n0 + r;
             const f32x4 x = kk < s.S ? *reinterpret_cast<const f32x4 *>(kb + (int64_t)kk * D + c)
                                      : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -316,7 +328,7 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
             for (int u = 0; u < 4; ++u) sm.kt[c + u][r] = x[u];
         }
     } else {
-        for (int i = tid; i < kBN * D; i += kThreads) {
+        for (int i = ptid; i < kBN * D; i += kThreads) {
             const int r = i % kBN, c = i / kBN, kk = n0 + r;
             sm.kt[c][r] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
         }
@@ -441,6 +453,8 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
         dq_product<D, kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
                       wave, lane);
 
+    const int etid = opaque_index(tid);  // the epilogue's own copy (see opaque_index)
+    const int elane = etid & 63, ekey = kw0 + (elane & 31), eg = elane >> 5;
     if (kv_atomic) {
         // A share of the tile's steps: dK and dV are added atomically.  Each wave's 32 x D block
         // goes through LDS first (the whole shared area is free after the last dQ product), so
@@ -456,11 +470,11 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
             for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; r += 4)
-                    *reinterpret_cast<f32x4 *>(blk + lr * RS + dt * 32 + acc_row(r, g)) =
+                    *reinterpret_cast<f32x4 *>(blk + (elane & 31) * RS + dt * 32 + acc_row(r, eg)) =
                         f32x4{acc[dt][r] * mul, acc[dt][r + 1] * mul, acc[dt][r + 2] * mul,
                               acc[dt][r + 3] * mul};
             __syncthreads();
-            for (int i = lane; i < rows * D; i += 64) {
+            for (int i = elane; i < rows * D; i += 64) {
                 const int rr = i / D, d = i % D;
                 if (d < s.E) unsafeAtomicAdd(dst + (int64_t)rr * s.E + d, blk[rr * RS + d]);
             }
@@ -471,14 +485,14 @@ DEVI void key_tile(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt, i
     }
 
     // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
-    if (key < s.S) {
-        float *dkr = kdst + (int64_t)(key - n0) * s.E;
-        float *dvr = vdst + (int64_t)(key - n0) * s.E;
+    if (ekey < s.S) {
+        float *dkr = kdst + (int64_t)(ekey - n0) * s.E;
+        float *dvr = vdst + (int64_t)(ekey - n0) * s.E;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; r += 4) {
-                const int d = dt * 32 + acc_row(r, g);
+                const int d = dt * 32 + acc_row(r, eg);
                 if (VEC) {
                     *reinterpret_cast<f32x4 *>(dkr + d) =
                         f32x4{dk[dt][r] * s.scale, dk[dt][r + 1] * s.scale,
@@ -531,21 +545,23 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
     const float *kb = static_cast<const float *>(a.k) + (int64_t)bhk * s.S * s.E;
     const float *vb = static_cast<const float *>(a.v) + (int64_t)bhk * s.S * s.E;
 
+    const int ptid = opaque_index(tid);  // the prologue's own copy (see opaque_index)
+    const int pkey = kw0 + (ptid & 15), pc4 = (ptid & 63) >> 4;
     // V of this lane's key at dims 16 j + 4 c4 + 0..3.
     f32x4 vreg[NKB];
 #pragma unroll
     for (int j = 0; j < NKB; ++j) {
-        const int d = 16 * j + 4 * c4;
-        if (VEC && key < s.S) {
-            vreg[j] = *reinterpret_cast<const f32x4 *>(vb + (int64_t)key * D + d);
+        const int d = 16 * j + 4 * pc4;
+        if (VEC && pkey < s.S) {
+            vreg[j] = *reinterpret_cast<const f32x4 *>(vb + (int64_t)pkey * D + d);
         } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) vreg[j][u] = (key < s.S && d + u < s.E) ? vb[(int64_t)key * s.E + d + u] : 0.f;
+            for (int u = 0; u < 4; ++u) vreg[j][u] = (pkey < s.S && d + u < s.E) ? vb[(int64_t)pkey * s.E + d + u] : 0.f;
         }
     }
     // The workgroup's K tile, transposed into LDS for the dQ product.
     if (VEC) {
-        for (int i = tid; i < kBN * (D / 4); i += NT) {
+        for (int i = ptid; i < kBN * (D / 4); i += NT) {
             const int r = i % kBN, c = (i / kBN) * 4, kk = n0 + r;
             const f32x4 x = kk < s.S ? *reinterpret_cast<const f32x4 *>(kb + (int64_t)kk * D + c)
                                      : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -553,7 +569,7 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
             for (int u = 0; u < 4; ++u) sm.kt[c + u][r] = x[u];
         }
     } else {
-        for (int i = tid; i < kBN * D; i += NT) {
+        for (int i = ptid; i < kBN * D; i += NT) {
             const int r = i % kBN, c = i / kBN, kk = n0 + r;
             sm.kt[c][r] = (kk < s.S && c < s.E) ? kb[(int64_t)kk * s.E + c] : 0.f;
         }
@@ -709,6 +725,8 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
         dq_product<D, 2 * kThreads>(sm, dq_dst(prev_bh, prev_m0), dq_atomic, s.L - prev_m0, step_keys(prev_m0), s.E, s.scale,
                       wave, lane);
 
+    const int etid = opaque_index(tid);  // the epilogue's own copy (see opaque_index)
+    const int elane = etid & 63, er16 = elane & 15, ec4 = elane >> 4, ekey = kw0 + er16;
     if (kv_atomic) {
         // As in key_tile: each wave's 16 x D block goes through LDS, then one atomic per element
         // along consecutive dims of one key.
@@ -720,10 +738,10 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
             __syncthreads();  // the previous readers of the area are done
 #pragma unroll
             for (int j = 0; j < NKB; ++j)
-                *reinterpret_cast<f32x4 *>(blk + r16 * RS + 16 * j + 4 * c4) =
+                *reinterpret_cast<f32x4 *>(blk + er16 * RS + 16 * j + 4 * ec4) =
                     f32x4{acc[j][0] * mul, acc[j][1] * mul, acc[j][2] * mul, acc[j][3] * mul};
             __syncthreads();
-            for (int i = lane; i < rows * D; i += 64) {
+            for (int i = elane; i < rows * D; i += 64) {
                 const int rr = i / D, d = i % D;
                 if (d < s.E) unsafeAtomicAdd(dst + (int64_t)rr * s.E + d, blk[rr * RS + d]);
             }
@@ -734,12 +752,12 @@ DEVI void key_tile16(const BwdArgs &a, BwdSmem<D> &sm, int tid, int bhk, int kt,
     }
 
     // dK = scale * dK^T^T, dV = dV^T^T for this lane's key.
-    if (key < s.S) {
-        float *dkr = kdst + (int64_t)(key - n0) * s.E;
-        float *dvr = vdst + (int64_t)(key - n0) * s.E;
+    if (ekey < s.S) {
+        float *dkr = kdst + (int64_t)(ekey - n0) * s.E;
+        float *dvr = vdst + (int64_t)(ekey - n0) * s.E;
 #pragma unroll
         for (int j = 0; j < NKB; ++j) {
-            const int d = 16 * j + 4 * c4;
+            const int d = 16 * j + 4 * ec4;
             if (VEC) {
                 *reinterpret_cast<f32x4 *>(dkr + d) =
                     f32x4{dk[j][0] * s.scale, dk[j][1] * s.scale, dk[j][2] * s.scale, dk[j][3] * s.scale};
