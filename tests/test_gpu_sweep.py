@@ -7,7 +7,9 @@ through `_native` (the C ABI), and compares out, lse, dq, dk, dv with the oracle
 inputs: float32 to |gpu - ref| <= 2e-5 + 1e-5 |ref|, bf16 (inputs rounded to bf16, the oracle's
 backward given the GPU's bf16 out and lse) to |gpu - ref| <= 1e-2 |ref| + 1e-2 rms(ref).  Few heads
 with long rows take the split forward, the stream-K / split backward; many short rows take the
-whole-tile grids, so the sweep crosses every schedule of both dtypes.
+whole-tile grids, so the sweep crosses every schedule of both dtypes.  A second sweep draws
+explicit scales (including negative and zero ones, whose causal calls have the reference's NaN
+rows) and head dims up to 256 (the bf16 flash kernels at 256, the float32 materialized path).
 """
 import numpy as np
 import pytest
@@ -82,3 +84,79 @@ def test_random_shapes(oracle_lib, i):
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv"), got, ref):
         check(a.float().cpu().numpy(), b, f"sweep {i} {name}")
+
+
+N_SCALED = 64
+
+
+def _scaled_case(i):
+    """Explicit scales (a multiple of 1/sqrt(E) from 0.1 to 2, negative, zero, or None) and head
+    dims up to 256, so that the draw also reaches the bf16 flash kernels at head dim 256 and the
+    float32 materialized path above 128."""
+    rng = np.random.default_rng(7000 + i)
+    B = int(rng.integers(1, 3))
+    H = int(rng.choice([1, 2, 4]))
+    Hkv = int(rng.choice([d for d in range(1, H + 1) if H % d == 0]))
+    L, S = int(rng.integers(1, 701)), int(rng.integers(1, 701))
+    E = int(rng.choice([1, 16, 64, 100, 128, 129, 160, 192, 200, 256]))
+    causal = bool(rng.random() < 0.5)
+    mask = str(rng.choice(["none", "none", "padding", "float"]))
+    dtype = "bf16" if rng.random() < 0.5 else "f32"
+    u = rng.random()
+    if u < 0.3:
+        scale = None
+    elif u < 0.8:
+        scale = float(rng.uniform(0.1, 2.0)) / float(np.sqrt(E))
+    elif u < 0.95:
+        scale = -float(rng.uniform(0.1, 2.0)) / float(np.sqrt(E))
+    else:
+        scale = 0.0
+    return dict(B=B, H=H, Hkv=Hkv, L=L, S=S, E=E, causal=causal, mask=mask, dtype=dtype, scale=scale,
+                seed=7000 + i)
+
+
+@pytest.mark.parametrize("i", range(N_SCALED))
+def test_random_shapes_scaled_wide(oracle_lib, i):
+    """As test_random_shapes, with explicit scales and head dims up to 256.  A causal call with a
+    scale that is not positive has the reference's NaN rows (its -inf causal fill is scaled before
+    the row max), so every comparison asks for the oracle's NaN elements exactly and the bar on
+    the others."""
+    from densecore_amd import _native
+    from tests._data import assert_bf16_nan, assert_f32_nan
+    c = _scaled_case(i)
+    B, H, Hkv, L, S, E, causal, scale = c["B"], c["H"], c["Hkv"], c["L"], c["S"], c["E"], c["causal"], c["scale"]
+    print(f"[case] scaled sweep {i}: {c}", flush=True)
+    rng = np.random.default_rng(c["seed"] + 1)
+    q, g = (rng.standard_normal((B, H, L, E), dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal((B, Hkv, S, E), dtype=np.float32) for _ in range(2))
+    bf16 = c["dtype"] == "bf16"
+    if bf16:
+        q, g, k, v = (bf16_round(x) for x in (q, g, k, v))
+    mask_np, mask_t = None, None
+    if c["mask"] == "padding":
+        lengths = rng.integers(1, S + 1, size=B)
+        row = np.where(np.arange(S)[None, :] < lengths[:, None], np.float32(0), np.float32(-np.inf))
+        mask_np = np.ascontiguousarray(np.broadcast_to(row[:, None, None, :], (B, H, L, S)), np.float32)
+        mask_t = torch.from_numpy(row[:, None, None, :].copy()).to(DEV).expand(B, H, L, S)
+    elif c["mask"] == "float":
+        mask_np = rng.standard_normal((B, H, L, S), dtype=np.float32)
+        mask_np[rng.random((B, H, L, S)) < 0.15] = -np.inf
+        mask_t = torch.from_numpy(mask_np).to(DEV)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tq, tk, tv, tg = (_t(x, dt) for x in (q, k, v, g))
+    out, lse = _native._flash_attention(tq, tk, tv, causal, scale, mask_t)
+    torch.cuda.synchronize()
+    ref_o, ref_l = oracle_lib.forward(q, k, v, causal, scale, mask_np)
+    check = assert_bf16_nan if bf16 else assert_f32_nan
+    check(out.float().cpu().numpy(), ref_o, f"scaled sweep {i} out")
+    check(lse.cpu().numpy(), ref_l, f"scaled sweep {i} lse")
+    if bf16:
+        o_in, l_in = out, lse
+        ref = oracle_lib.backward(g, q, k, v, out.float().cpu().numpy(), lse.cpu().numpy(), causal, scale, mask_np)
+    else:
+        o_in, l_in = _t(ref_o, dt), torch.from_numpy(ref_l).to(DEV)
+        ref = oracle_lib.backward(g, q, k, v, ref_o, ref_l, causal, scale, mask_np)
+    got = _native._flash_attention_backward(tg, tq, tk, tv, o_in, l_in, causal, scale, mask_t)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        check(a.float().cpu().numpy(), b, f"scaled sweep {i} {name}")
