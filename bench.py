@@ -484,7 +484,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
-              "path shards over (batch, head) with no collectives, see DESIGN.md", file=sys.stderr)
+              "path shards over (batch, head) with no collectives, each GPU running its share of "
+              "the heads on its own", file=sys.stderr)
         sys.exit(2)
 
     import torch
