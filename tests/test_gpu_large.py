@@ -43,6 +43,8 @@ def test_kv_over_2_31_elements(dtype):
     k = torch.randn(B, H, S, E, device=DEV, generator=gen, dtype=dt)
     v = torch.randn(B, H, S, E, device=DEV, generator=gen, dtype=dt)
     try:
+        if dtype == "f32":  # the deterministic slots (4.3 GB) exceed the bound: pieces of kv heads
+            assert _native._schedule(True, q, k, v, False)["chunks"] > 1
         out, lse = _native._flash_attention(q, k, v, False)
         dq, dk, dv = _native._flash_attention_backward(g, q, k, v, out, lse, False)
         torch.cuda.synchronize()
