@@ -86,3 +86,49 @@ def test_kv_over_2_31_elements(dtype):
         del q, g, k, v
         _native.release_workspaces()
         torch.cuda.empty_cache()
+
+
+LQ, SQ = (1 << 20) + 64, 64
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_q_over_2_31_elements(dtype):
+    """The query side: Q, dO, out and dQ of 16 heads x 1,048,640 queries x 128 dims (more than 2^31
+    elements) over 64 keys, non-causal; the last head checked in float64 NumPy (out, lse and dQ of
+    every query, dK and dV of every key)."""
+    from densecore_amd import _native
+    assert B * H * LQ * E > 1 << 31
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    rel = 1e-2 if dtype == "bf16" else 1e-4
+    print(f"[case] large Q {dtype} B{B} H{H} L{LQ} S{SQ} E{E} non-causal", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(232)
+    q = torch.randn(B, H, LQ, E, device=DEV, generator=gen, dtype=dt)
+    g = torch.randn(B, H, LQ, E, device=DEV, generator=gen, dtype=dt)
+    k = torch.randn(B, H, SQ, E, device=DEV, generator=gen, dtype=dt)
+    v = torch.randn(B, H, SQ, E, device=DEV, generator=gen, dtype=dt)
+    try:
+        out, lse = _native._flash_attention(q, k, v, False)
+        dq, dk, dv = _native._flash_attention_backward(g, q, k, v, out, lse, False)
+        torch.cuda.synchronize()
+
+        hh = H - 1
+        f64 = lambda t: t[0, hh].float().cpu().numpy().astype(np.float64)
+        qh, gh, kh, vh = f64(q), f64(g), f64(k), f64(v)
+        scale = 1.0 / np.sqrt(E)
+        s = (qh @ kh.T) * scale                       # (LQ, SQ)
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        lsum = p.sum(axis=1, keepdims=True)
+        _check(out[0, hh].float().cpu().numpy(), (p @ vh) / lsum, rel, "out")
+        _check(lse[0, hh].cpu().numpy(), (m + np.log(lsum))[:, 0], rel, "lse")
+        oh = f64(out)
+        lh = lse[0, hh].cpu().numpy().astype(np.float64)
+        p = np.exp(s - lh[:, None])
+        ds = p * (gh @ vh.T - (gh * oh).sum(axis=1, keepdims=True))
+        _check(dq[0, hh].float().cpu().numpy(), scale * (ds @ kh), rel, "dq")
+        _check(dk[0, hh].float().cpu().numpy(), scale * (ds.T @ qh), rel, "dk")
+        _check(dv[0, hh].float().cpu().numpy(), p.T @ gh, rel, "dv")
+    finally:
+        del q, g, k, v
+        _native.release_workspaces()
+        torch.cuda.empty_cache()
