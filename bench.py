@@ -11,7 +11,9 @@ metric names (C4, dc_sdpa_decode, GB/s of K + V + q + out + lse), the other conf
 throughput (wall clock over K steps between two synchronizations, each config warmed up for at
 least W steps and 100 ms of its own work, so that it is timed at steady clocks), a roofline entry per
 entry point whose kernel time comes from HIP events on the launch stream around back-to-back
-calls of that entry point alone, and the CPU baseline: the oracle (a C port of DenseCore's CPU path) timed on this host.
+calls of that entry point alone (``in_step`` gives the same entry points timed inside the step, by
+events in a separate loop of the same steps), and the CPU baseline: the oracle (a C port of
+DenseCore's CPU path) timed on this host.
 C2 runs last, straight after C1's GPU work (float32 MFMA work like its own) with its inputs already
 on the device, so that its W warm-up steps start at the clocks the device holds under that load.
 ``math_path`` reports the composed path's own kernels (softmax forward/backward, the Bernoulli
@@ -88,6 +90,27 @@ def kernel_ms(torch, stream, fn, n):
     b.record(stream)
     b.synchronize()
     return a.elapsed_time(b) / n
+
+
+def in_step_ms(torch, stream, fwd, bwd, n):
+    """Mean per-entry-point time inside the step itself: n more steps, with pre-made HIP events
+    recorded before the forward, between it and the backward, and after (a separate loop, so the
+    timed steps carry no event packets).  Their sum is the step's GPU time plus the events' own
+    cost (a few us per interval on this part), against which ms_per_step can be compared."""
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3 if bwd else 2)] for _ in range(n)]
+    for e in ev:
+        e[0].record(stream)
+        out, lse = fwd()
+        e[1].record(stream)
+        if bwd is not None:
+            bwd(out, lse)
+            e[2].record(stream)
+    torch.cuda.synchronize()
+    f = sum(e[0].elapsed_time(e[1]) for e in ev) / n
+    if bwd is None:
+        return {"fwd_ms": round(f, 4), "steps": n}
+    b = sum(e[1].elapsed_time(e[2]) for e in ev) / n
+    return {"fwd_ms": round(f, 4), "bwd_ms": round(b, 4), "sum_ms": round(f + b, 4), "steps": n}
 
 
 def roofline(achieved, peak, unit, bound, traffic, kernel, work_note):
@@ -177,10 +200,13 @@ def bench_prefill(torch, native, name, steps, warmup, dev, inputs=None):
         step()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
-    # Per-entry-point kernel time, for the roofline: the same calls, back to back.
+    # Per-entry-point kernel time, for the roofline: the same calls, back to back; and the same
+    # steps with an event pair around each entry point.
     n = max(steps, 10)
     res = {"ms_per_step": wall, "fwd_ms": kernel_ms(torch, stream, fwd, n), "bwd_ms": 0.0,
            "timing_calls": n}
+    res["in_step"] = in_step_ms(torch, stream, fwd, (lambda o, l: native._flash_attention_backward(
+        g, q, k, v, o, l, causal, scale, mask)) if bwd else None, n)
     if bwd:
         out, lse = fwd()
         res["bwd_ms"] = kernel_ms(torch, stream, lambda: native._flash_attention_backward(
@@ -554,6 +580,7 @@ def main():
             f"{c2['fwd_flop'] / 1e9:.3f} GFLOP per call / {c2['fwd_ms']:.4f} ms (HIP events around "
             f"{c2['timing_calls']} back-to-back calls)")
         line["mfma_frac"] = round(c2["tflops"] / PEAK_FP32_MFMA, 4)
+        line["in_step"] = c2["in_step"]
         line["public_api"] = c2["public"]
     c4 = results.get("C4")
     if c4:
@@ -579,6 +606,7 @@ def main():
                         "frac": round(r["tflops"] / peak, 4), "fwd_ms": round(r["fwd_ms"], 4)}
         if r.get("bwd_ms"):
             others[name]["bwd_ms"] = round(r["bwd_ms"], 4)
+        others[name]["in_step"] = r["in_step"]
     if others:
         line["other_configs"] = others
     if results.get("math"):
