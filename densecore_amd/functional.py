@@ -300,6 +300,11 @@ def _float_mask(mask):
     return mask
 
 
+def _append_position(mask):
+    """A mask over the keys with one more key at the end, always visible (a zero column)."""
+    return None if mask is None else torch.nn.functional.pad(mask, (0, 1))
+
+
 def multi_head_attention_forward(query, key, value, embed_dim_to_check, num_heads, in_proj_weight,
                                  in_proj_bias, bias_k, bias_v, add_zero_attn, dropout_p,
                                  out_proj_weight, out_proj_bias, training=True,
@@ -307,61 +312,81 @@ def multi_head_attention_forward(query, key, value, embed_dim_to_check, num_head
                                  use_separate_proj_weight=False, q_proj_weight=None,
                                  k_proj_weight=None, v_proj_weight=None, static_k=None,
                                  static_v=None, average_attn_weights=True, is_causal=False):
-    """PyTorch's reference algorithm as ``functional.py:400-461`` composes it, on the GPU.
-    Inputs are (L, N, E), or (L, E) unbatched.  ``is_causal`` is only a hint: ``attn_mask``
-    must still be given and is the one applied.  The input and output projections are device
-    BLAS calls (``F.linear``); the two batched products are this library's ``bmm``, the mask add
-    and softmax (no safe rows here, as in the reference) its softmax kernel, and dropout its
-    dropout."""
+    """Multi-head attention with PyTorch's ``F.multi_head_attention_forward`` signature and
+    semantics (the reference composes the same steps, ``functional.py:400-461``), on the GPU.
+
+    query is (L, N, E) or unbatched (L, E); key and value (S, N, kdim / vdim) or (S, kdim / vdim).
+    The steps, in PyTorch's order: project q, k, v (the packed ``in_proj_weight`` holds the three
+    projections in that order, or the three separate weights); append ``bias_k`` / ``bias_v`` as
+    one more key position; split the heads; substitute ``static_k`` / ``static_v``; append a zero
+    key position (``add_zero_attn``); fold ``key_padding_mask`` into the additive mask; attention
+    weights softmax(q k^T / sqrt(head_dim) + mask), dropped out when training; their product with
+    v, merged heads, output projection.  Masks that gain a key position gain a zero column.  Bool
+    masks are True where attention is not allowed.  ``is_causal`` is only a hint: ``attn_mask``
+    must still be given, and is what is applied.  The projections are device BLAS calls
+    (``F.linear``); the two batched products are this library's ``bmm``, the mask add and the
+    softmax its softmax kernel (rows whose keys are all masked come out NaN, as PyTorch's do), and
+    the dropout its dropout."""
     F = torch.nn.functional
     if is_causal and attn_mask is None:
         raise RuntimeError("Need attn_mask if specifying the is_causal hint")
-    batched = query.dim() == 3
-    if not batched:
-        query, key, value = query.unsqueeze(1), key.unsqueeze(1), value.unsqueeze(1)
-        if key_padding_mask is not None:
-            key_padding_mask = key_padding_mask.unsqueeze(0)
-    tgt_len, bsz, embed_dim = query.shape
+    unbatched = query.dim() != 3
+    if unbatched:  # one sequence: a batch of one along dim 1
+        query, key, value = (x.unsqueeze(1) for x in (query, key, value))
+        key_padding_mask = None if key_padding_mask is None else key_padding_mask.unsqueeze(0)
+    tgt_len, batch, embed_dim = query.shape
     if embed_dim != embed_dim_to_check:
         raise ValueError(f"was expecting embedding dimension of {embed_dim_to_check}, but got {embed_dim}")
     head_dim = embed_dim // num_heads
-    biases = (None, None, None) if in_proj_bias is None else in_proj_bias.chunk(3)
-    weights = ((q_proj_weight, k_proj_weight, v_proj_weight) if use_separate_proj_weight
-               else in_proj_weight.chunk(3))
-    q, k, v = (F.linear(x, w, b) for x, w, b in zip((query, key, value), weights, biases))
-    attn_mask = _float_mask(attn_mask)
-    if attn_mask is not None and attn_mask.dim() == 2:
-        attn_mask = attn_mask.unsqueeze(0)
-    key_padding_mask = _float_mask(key_padding_mask)
+    rows = batch * num_heads
+
+    # Input projections.
+    if use_separate_proj_weight:
+        proj_w = (q_proj_weight, k_proj_weight, v_proj_weight)
+    else:
+        proj_w = in_proj_weight.chunk(3)
+    proj_b = in_proj_bias.chunk(3) if in_proj_bias is not None else (None, None, None)
+    q = F.linear(query, proj_w[0], proj_b[0])
+    k = F.linear(key, proj_w[1], proj_b[1])
+    v = F.linear(value, proj_w[2], proj_b[2])
+
+    mask = _float_mask(attn_mask)
+    if mask is not None and mask.dim() == 2:
+        mask = mask.unsqueeze(0)  # one (L, S) mask for every (batch, head)
+    key_pad = _float_mask(key_padding_mask)
     if bias_k is not None and bias_v is not None:
-        k = torch.cat([k, bias_k.expand(1, bsz, embed_dim)])
-        v = torch.cat([v, bias_v.expand(1, bsz, embed_dim)])
-        attn_mask = None if attn_mask is None else F.pad(attn_mask, (0, 1))
-        key_padding_mask = None if key_padding_mask is None else F.pad(key_padding_mask, (0, 1))
-    q = q.reshape(tgt_len, bsz * num_heads, head_dim).transpose(0, 1)
-    k = static_k if static_k is not None else k.reshape(k.shape[0], bsz * num_heads, head_dim).transpose(0, 1)
-    v = static_v if static_v is not None else v.reshape(v.shape[0], bsz * num_heads, head_dim).transpose(0, 1)
+        k = torch.cat([k, bias_k.expand(1, batch, embed_dim)])
+        v = torch.cat([v, bias_v.expand(1, batch, embed_dim)])
+        mask, key_pad = _append_position(mask), _append_position(key_pad)
+
+    # (seq, batch, heads * head_dim) -> (batch * heads, seq, head_dim)
+    def heads(x):
+        return x.reshape(x.shape[0], rows, head_dim).transpose(0, 1)
+
+    q = heads(q)
+    k = heads(k) if static_k is None else static_k
+    v = heads(v) if static_v is None else static_v
     if add_zero_attn:
-        k = torch.cat([k, k.new_zeros(bsz * num_heads, 1, head_dim)], 1)
-        v = torch.cat([v, v.new_zeros(bsz * num_heads, 1, head_dim)], 1)
-        attn_mask = None if attn_mask is None else F.pad(attn_mask, (0, 1))
-        key_padding_mask = None if key_padding_mask is None else F.pad(key_padding_mask, (0, 1))
+        k = torch.cat([k, k.new_zeros(rows, 1, head_dim)], 1)
+        v = torch.cat([v, v.new_zeros(rows, 1, head_dim)], 1)
+        mask, key_pad = _append_position(mask), _append_position(key_pad)
     src_len = k.shape[1]
-    if key_padding_mask is not None:
-        padding = key_padding_mask.reshape(bsz, 1, 1, src_len).expand(bsz, num_heads, 1, src_len)
-        padding = padding.reshape(bsz * num_heads, 1, src_len)
-        attn_mask = padding if attn_mask is None else attn_mask + padding
-    scores = bmm(q * math.sqrt(1.0 / head_dim), k.transpose(1, 2))
-    probabilities = softmax_masked(scores, attn_mask, safe=False)
+    if key_pad is not None:
+        per_row = key_pad.reshape(batch, 1, 1, src_len).expand(batch, num_heads, 1, src_len)
+        per_row = per_row.reshape(rows, 1, src_len)
+        mask = per_row if mask is None else mask + per_row
+
+    attn = softmax_masked(bmm(q * math.sqrt(1.0 / head_dim), k.transpose(1, 2)), mask, safe=False)
     if training and dropout_p > 0:
-        probabilities = dropout(probabilities, dropout_p, True)
-    out = bmm(probabilities, v).transpose(0, 1).reshape(tgt_len * bsz, embed_dim)
-    out = F.linear(out, out_proj_weight, out_proj_bias).reshape(tgt_len, bsz, -1)
-    if not batched:
+        attn = dropout(attn, dropout_p, True)
+    merged = bmm(attn, v).transpose(0, 1).reshape(tgt_len * batch, embed_dim)
+    out = F.linear(merged, out_proj_weight, out_proj_bias).reshape(tgt_len, batch, -1)
+    if unbatched:
         out = out.squeeze(1)
     if not need_weights:
         return out, None
-    probabilities = probabilities.reshape(bsz, num_heads, tgt_len, src_len)
+    attn = attn.reshape(batch, num_heads, tgt_len, src_len)
     if average_attn_weights:
-        probabilities = probabilities.mean(1)
-    return out, probabilities if batched else probabilities.squeeze(0)
+        attn = attn.mean(1)
+    return out, attn.squeeze(0) if unbatched else attn
+

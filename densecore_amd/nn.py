@@ -1,11 +1,12 @@
-"""``nn.MultiheadAttention`` on the GPU (``python/densecore/nn.py:595-640`` of the reference).
+"""``nn.MultiheadAttention`` on the GPU (the reference's module: ``python/densecore/nn.py:595-640``).
 
-Same constructor arguments, parameter names and shapes, initialisation rules (xavier-uniform
-projection weights, zero projection biases, zero ``out_proj.bias``, xavier-normal ``bias_k`` /
-``bias_v``) and forward as the reference module; the parameters live on the GPU and the forward
-is ``functional.multi_head_attention_forward``.  Initial values come from torch's generator
-(the reference draws them from its own CPU generator), so two freshly built modules agree in
-distribution, not in bits: load the same weights to compare outputs.
+The module follows PyTorch's documented ``torch.nn.MultiheadAttention``: its constructor
+arguments, its parameters (names, shapes, and which of them exist for a given configuration) and
+its initialisation (``_reset_parameters``: xavier-uniform input projections, zero input and
+output projection biases, xavier-normal ``bias_k`` / ``bias_v``), with the parameters on the GPU
+and the forward through ``functional.multi_head_attention_forward``.  Initial values come from
+torch's generator (the reference draws them from its own CPU generator), so two freshly built
+modules agree in distribution, not in bits: load the same weights to compare outputs.
 """
 import torch
 
@@ -13,7 +14,9 @@ from . import functional
 
 
 class MultiheadAttention(torch.nn.Module):
-    """torch.nn.MultiheadAttention: same parameters, initialization and forward."""
+    """Multi-head attention (Q, K, V projections, ``num_heads`` heads of ``embed_dim //
+    num_heads`` dims, output projection) with PyTorch's parameterisation; forward returns
+    ``(attn_output, attn_weights)``, the weights averaged over heads unless asked otherwise."""
 
     def __init__(self, embed_dim, num_heads, dropout=0.0, bias=True, add_bias_kv=False,
                  add_zero_attn=False, kdim=None, vdim=None, batch_first=False, device=None,
@@ -23,49 +26,63 @@ class MultiheadAttention(torch.nn.Module):
             raise ValueError("embed_dim and num_heads must be greater than 0")
         if embed_dim % num_heads:
             raise AssertionError("embed_dim must be divisible by num_heads")
-        device = torch.device("cuda") if device is None else torch.device(device)
-        dtype = torch.float32 if dtype is None else dtype
-        self.embed_dim, self.num_heads, self.dropout = embed_dim, num_heads, dropout
+        where = {"device": torch.device("cuda") if device is None else torch.device(device),
+                 "dtype": torch.float32 if dtype is None else dtype}
+        self.embed_dim = embed_dim
+        self.num_heads = num_heads
+        self.head_dim = embed_dim // num_heads
+        self.dropout = dropout
         self.batch_first = batch_first
-        self.kdim, self.vdim = kdim or embed_dim, vdim or embed_dim
+        self.add_zero_attn = add_zero_attn
+        self.kdim = kdim if kdim else embed_dim
+        self.vdim = vdim if vdim else embed_dim
+        # One packed (3E, E) input projection when keys and values have the query's width.
         self._qkv_same_embed_dim = self.kdim == embed_dim and self.vdim == embed_dim
-        self.head_dim, self.add_zero_attn = embed_dim // num_heads, add_zero_attn
 
-        def empty(*shape):
-            return torch.nn.Parameter(torch.zeros(shape, device=device, dtype=dtype))
+        def param(*shape):
+            return torch.nn.Parameter(torch.empty(shape, **where))
 
+        packed = self._qkv_same_embed_dim
+        self.in_proj_weight = param(3 * embed_dim, embed_dim) if packed else None
+        self.q_proj_weight = None if packed else param(embed_dim, embed_dim)
+        self.k_proj_weight = None if packed else param(embed_dim, self.kdim)
+        self.v_proj_weight = None if packed else param(embed_dim, self.vdim)
+        self.in_proj_bias = param(3 * embed_dim) if bias else None
+        self.out_proj = torch.nn.Linear(embed_dim, embed_dim, bias=bias, **where)
+        self.bias_k = param(1, 1, embed_dim) if add_bias_kv else None
+        self.bias_v = param(1, 1, embed_dim) if add_bias_kv else None
+        self._reset_parameters()
+
+    def _reset_parameters(self):
+        """PyTorch's initial values: xavier-uniform input projection weight(s), zero input and
+        output projection biases (the output projection's weight keeps ``Linear``'s own
+        initialisation), xavier-normal ``bias_k`` and ``bias_v``."""
+        init = torch.nn.init
         if self._qkv_same_embed_dim:
-            self.in_proj_weight = empty(3 * embed_dim, embed_dim)
-            self.q_proj_weight = self.k_proj_weight = self.v_proj_weight = None
+            init.xavier_uniform_(self.in_proj_weight)
         else:
-            self.q_proj_weight = empty(embed_dim, embed_dim)
-            self.k_proj_weight = empty(embed_dim, self.kdim)
-            self.v_proj_weight = empty(embed_dim, self.vdim)
-            self.in_proj_weight = None
-        self.in_proj_bias = empty(3 * embed_dim) if bias else None
-        self.out_proj = torch.nn.Linear(embed_dim, embed_dim, bias=bias, device=device, dtype=dtype)
-        self.bias_k, self.bias_v = ((empty(1, 1, embed_dim), empty(1, 1, embed_dim)) if add_bias_kv
-                                    else (None, None))
-        for weight in (self.in_proj_weight, self.q_proj_weight, self.k_proj_weight, self.v_proj_weight):
-            if weight is not None:
-                torch.nn.init.xavier_uniform_(weight)
-        if bias:
-            torch.nn.init.zeros_(self.out_proj.bias)
-        for extra in (self.bias_k, self.bias_v):
-            if extra is not None:
-                torch.nn.init.xavier_normal_(extra)
+            for w in (self.q_proj_weight, self.k_proj_weight, self.v_proj_weight):
+                init.xavier_uniform_(w)
+        if self.in_proj_bias is not None:
+            init.zeros_(self.in_proj_bias)
+            init.zeros_(self.out_proj.bias)
+        if self.bias_k is not None:
+            init.xavier_normal_(self.bias_k)
+            init.xavier_normal_(self.bias_v)
 
     def forward(self, query, key, value, key_padding_mask=None, need_weights=True, attn_mask=None,
                 average_attn_weights=True, is_causal=False):
-        batched = query.dim() == 3
-        if self.batch_first and batched:
-            query, key, value = (x.transpose(1, 0) for x in (query, key, value))
+        # batch_first inputs (N, L, E) go through the functional form as (L, N, E) and back.
+        swap = self.batch_first and query.dim() == 3
+        if swap:
+            query, key, value = query.transpose(0, 1), key.transpose(0, 1), value.transpose(0, 1)
         out, weights = functional.multi_head_attention_forward(
-            query, key, value, self.embed_dim, self.num_heads, self.in_proj_weight, self.in_proj_bias,
-            self.bias_k, self.bias_v, self.add_zero_attn, self.dropout, self.out_proj.weight,
-            self.out_proj.bias, training=self.training, key_padding_mask=key_padding_mask,
-            need_weights=need_weights, attn_mask=attn_mask,
-            use_separate_proj_weight=not self._qkv_same_embed_dim, q_proj_weight=self.q_proj_weight,
-            k_proj_weight=self.k_proj_weight, v_proj_weight=self.v_proj_weight,
-            average_attn_weights=average_attn_weights, is_causal=is_causal)
-        return (out.transpose(1, 0) if self.batch_first and batched else out), weights
+            query, key, value, self.embed_dim, self.num_heads, self.in_proj_weight,
+            self.in_proj_bias, self.bias_k, self.bias_v, self.add_zero_attn, self.dropout,
+            self.out_proj.weight, self.out_proj.bias, training=self.training,
+            key_padding_mask=key_padding_mask, need_weights=need_weights, attn_mask=attn_mask,
+            use_separate_proj_weight=not self._qkv_same_embed_dim,
+            q_proj_weight=self.q_proj_weight, k_proj_weight=self.k_proj_weight,
+            v_proj_weight=self.v_proj_weight, average_attn_weights=average_attn_weights,
+            is_causal=is_causal)
+        return (out.transpose(0, 1) if swap else out), weights

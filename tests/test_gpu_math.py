@@ -256,3 +256,23 @@ def test_math_path_empty_dims(shape, causal):
         assert t.grad is not None and tuple(t.grad.shape) == s
     if qs[-1] == 0 and out.numel():
         assert_f32(_np(tv.grad), np.matmul(np.swapaxes(w, -1, -2), g).astype(np.float32), "E = 0 dv")
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(bias=False), dict(add_bias_kv=True), dict(kdim=40, vdim=24),
+                                dict(add_zero_attn=True, batch_first=True)])
+def test_multi_head_attention_parameters_as_torch(kw):
+    """The module's parameters are torch.nn.MultiheadAttention's: the same names and shapes for
+    the same arguments, and its initial rules (zero projection biases, xavier-scaled weights)."""
+    from densecore_amd import nn
+    E, heads = 64, 4
+    ours = nn.MultiheadAttention(E, heads, **kw)
+    theirs = torch.nn.MultiheadAttention(E, heads, device=DEV, **kw)
+    got = {n: tuple(p.shape) for n, p in ours.named_parameters()}
+    want = {n: tuple(p.shape) for n, p in theirs.named_parameters()}
+    assert got == want
+    if kw.get("bias", True):
+        assert not ours.in_proj_bias.any() and not ours.out_proj.bias.any()
+    for n, p in ours.named_parameters():
+        if n.endswith("proj_weight"):  # xavier-uniform: |w| <= sqrt(6 / (fan_in + fan_out))
+            bound = (6.0 / (p.shape[0] + p.shape[1])) ** 0.5
+            assert float(p.abs().max()) <= bound and float(p.abs().max()) > 0.5 * bound, n
