@@ -591,43 +591,44 @@ hipError_t launch_dv(const FwdArgs &a, hipStream_t st) {
         if (a.s.causal) return launch(fwd_bf16_kernel<D, true, false, VEC>, grid, block, st, a);
         if (mask) return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
         return launch(fwd_bf16_kernel<D, false, false, VEC>, grid, block, st, a);
-    }
-    if (!mask) {
-        const int nqt = (a.s.L + kPPM - 1) / kPPM;
-        const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
-        if (a.v16) {
-            record_schedule(f16_products, 1);
-            FwdArgs f = a;
-            const F16Copy vcopy{a.v, a.v16, (int64_t)a.s.S * a.s.E, a.vexp};
-            return_if(launch_to_f16(&vcopy, 1, (int64_t)a.s.B * a.s.Hkv, a.f16_partial, st));
-            f.v = a.v16;
-            if (a.split_o) {
-                const FwdSplitPlan p = plan<D>(a.s);
-                if (p.chunk > 0 && p.bytes <= a.split_bytes) {
-                    record_schedule(split_chunk, p.chunk);
-                    record_schedule(split_pieces, p.max_pieces);
-                    f.split_chunk = p.chunk, f.split_max = p.max_pieces;
-                    f.split_lse = f.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
-                    const dim3 sgrid((unsigned)p.blocks);
-                    if (a.s.causal)
-                        return_if(launch(fwd_bf16_pp_kernel<D, true, VEC, true, true>, sgrid, block, st, f));
-                    else
-                        return_if(launch(fwd_bf16_pp_kernel<D, false, VEC, true, true>, sgrid, block, st, f));
-                    const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
-                    return launch(fwd_split_merge_kernel<__bf16>, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, f,
-                                  kPPM, kBN);
+    } else {  // head dims up to 128 (the ping-pong kernel exists only there)
+        if (!mask) {
+            const int nqt = (a.s.L + kPPM - 1) / kPPM;
+            const dim3 grid(nqt * a.s.B * a.s.H), block(kPPThreads);
+            if (a.v16) {
+                record_schedule(f16_products, 1);
+                FwdArgs f = a;
+                const F16Copy vcopy{a.v, a.v16, (int64_t)a.s.S * a.s.E, a.vexp};
+                return_if(launch_to_f16(&vcopy, 1, (int64_t)a.s.B * a.s.Hkv, a.f16_partial, st));
+                f.v = a.v16;
+                if (a.split_o) {
+                    const FwdSplitPlan p = plan<D>(a.s);
+                    if (p.chunk > 0 && p.bytes <= a.split_bytes) {
+                        record_schedule(split_chunk, p.chunk);
+                        record_schedule(split_pieces, p.max_pieces);
+                        f.split_chunk = p.chunk, f.split_max = p.max_pieces;
+                        f.split_lse = f.split_o + (size_t)a.s.B * a.s.H * a.s.L * p.max_pieces * a.s.E;
+                        const dim3 sgrid((unsigned)p.blocks);
+                        if (a.s.causal)
+                            return_if(launch(fwd_bf16_pp_kernel<D, true, VEC, true, true>, sgrid, block, st, f));
+                        else
+                            return_if(launch(fwd_bf16_pp_kernel<D, false, VEC, true, true>, sgrid, block, st, f));
+                        const int64_t rows = (int64_t)a.s.B * a.s.H * a.s.L;
+                        return launch(fwd_split_merge_kernel<__bf16>, dim3((unsigned)((rows + 15) / 16)), dim3(256), st, f,
+                                      kPPM, kBN);
+                    }
                 }
+                if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, true>, grid, block, st, f);
+                return launch(fwd_bf16_pp_kernel<D, false, VEC, true>, grid, block, st, f);
             }
-            if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, true>, grid, block, st, f);
-            return launch(fwd_bf16_pp_kernel<D, false, VEC, true>, grid, block, st, f);
+            if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, false>, grid, block, st, a);
+            return launch(fwd_bf16_pp_kernel<D, false, VEC, false>, grid, block, st, a);
         }
-        if (a.s.causal) return launch(fwd_bf16_pp_kernel<D, true, VEC, false>, grid, block, st, a);
-        return launch(fwd_bf16_pp_kernel<D, false, VEC, false>, grid, block, st, a);
+        const int nqt = (a.s.L + kBM - 1) / kBM;
+        const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
+        if (a.s.causal) return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
+        return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
     }
-    const int nqt = (a.s.L + kBM - 1) / kBM;
-    const dim3 grid(nqt * a.s.B * a.s.H), block(kThreads);
-    if (a.s.causal) return launch(fwd_bf16_kernel<D, true, true, VEC>, grid, block, st, a);
-    return launch(fwd_bf16_kernel<D, false, true, VEC>, grid, block, st, a);
 }
 
 template <int D>
