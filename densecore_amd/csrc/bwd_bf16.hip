@@ -209,13 +209,22 @@ __global__ __launch_bounds__(KLayout<D>::THREADS) void bwd_dkdv_bf16_kernel(BwdA
     };
     // -lse log2 e (-inf past L: P = 0 there) and -dsum of a step, one value per lane of waves
     // 0 and 1.  (The float32 kernels subtract lse in natural-log units first, which saves one
-    // rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)
-    auto load_row_stat = [&](int i) -> float {
+    // rounding of size |lse| 2^-24 in the exponent; at bf16 precision it is noise.)  The global
+    // load (load_row_raw) and the arithmetic on it (row_stat) are apart so that the next step's
+    // load is issued at the top of a step and waited for at its end: computed at once, the value
+    // would make waves 0 and 1 wait out the load's latency before their step's work.
+    struct RowRaw {
+        float x;
+        bool in;  // the row is below L
+    };
+    auto load_row_raw = [&](int i) -> RowRaw {
         const int bh = step_bh(i), qq = step_m0(i) + lane;
-        if (wave == 0)
-            return qq < s.L ? -a.lse[(int64_t)bh * s.L + qq] * kLog2e + (F16 ? (float)(kPShift - kDsShift) : 0.f)
-                            : -INFINITY;
-        const float ds = qq < s.L ? -a.dsum[(int64_t)bh * s.L + qq] : 0.f;
+        if (qq >= s.L) return {0.f, false};
+        return {wave == 0 ? a.lse[(int64_t)bh * s.L + qq] : a.dsum[(int64_t)bh * s.L + qq], true};
+    };
+    auto row_stat = [&](RowRaw r) -> float {
+        if (wave == 0) return r.in ? -r.x * kLog2e + (F16 ? (float)(kPShift - kDsShift) : 0.f) : -INFINITY;
+        const float ds = r.in ? -r.x : 0.f;
         return F16 ? ldexpf(ds, fs.e_pv) : ds;
     };
     auto store_row_stat = [&](int i, float x) {
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(KLayout<D>::THREADS) void bwd_dkdv_bf16_kernel(BwdA
     };
     if (QB == 2 && i_begin < nsteps) {
         fill_step(i_begin);
-        if (wave < 2) store_row_stat(i_begin, load_row_stat(i_begin));
+        if (wave < 2) store_row_stat(i_begin, row_stat(load_row_raw(i_begin)));
     }
 
     const uint32_t rowb = row_lanebase<kKM, D>(lane);
@@ -239,19 +248,19 @@ __global__ __launch_bounds__(KLayout<D>::THREADS) void bwd_dkdv_bf16_kernel(BwdA
 
     for (int i = i_begin; i < nsteps; ++i) {
         const int bh = step_bh(i), h = bh - b * s.H, m0 = step_m0(i), buf = i % QB;
-        float stat = 0.f;
+        RowRaw stat = {0.f, false};
         if constexpr (QB == 2) {
             if (VEC) wait_vmem();
             __syncthreads();  // step i's tiles landed (and K/V at i = 0); step i - 1 is done
             if (i + 1 < nsteps) {
-                if (wave < 2) stat = load_row_stat(i + 1);
+                if (wave < 2) stat = load_row_raw(i + 1);
                 fill_step(i + 1);
             }
         } else {
             // One buffer: step i's tiles are loaded once step i - 1 is done with the buffer.
             if (i > i_begin) __syncthreads();
             fill_step(i);
-            if (wave < 2) store_row_stat(i, load_row_stat(i));
+            if (wave < 2) store_row_stat(i, row_stat(load_row_raw(i)));
             if (VEC) wait_vmem();
             __syncthreads();  // step i's tiles landed (and K/V at the first step)
         }
@@ -359,7 +368,7 @@ __global__ __launch_bounds__(KLayout<D>::THREADS) void bwd_dkdv_bf16_kernel(BwdA
                 }
             }
         }
-        if (QB == 2 && i + 1 < nsteps && wave < 2) store_row_stat(i + 1, stat);
+        if (QB == 2 && i + 1 < nsteps && wave < 2) store_row_stat(i + 1, row_stat(stat));
     }
 
     // Sum the two partials of each key group (waves kw and kw + 4) and write dK, dV.  The
